@@ -1,0 +1,335 @@
+// Token permutation kernels: bit-exact Hilbert gather / inverse scatter and
+// the fused preparation of the attention and scoring operands.
+//
+// Every row is a contiguous head_dim-element vector (256 bytes at d128 bf16),
+// moved with 16-byte accesses so one row is one fully coalesced segment.
+#include "common.h"
+
+namespace dfs {
+namespace {
+
+template <typename V>
+__global__ void __launch_bounds__(256) gather_rows_kernel(
+    const V* __restrict__ src, const int32_t* __restrict__ perm, V* __restrict__ dst,
+    int64_t src_rows, int n_perm, int dst_rows, int vpr) {
+  const int64_t h = blockIdx.y;
+  const V* s = src + h * src_rows * vpr;
+  V* d = dst + h * static_cast<int64_t>(dst_rows) * vpr;
+  const int total = dst_rows * vpr;
+  for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += gridDim.x * blockDim.x) {
+    const int r = idx / vpr;
+    const int c = idx - r * vpr;
+    V val{};
+    if (r < n_perm) {
+      const int pr = perm[r];
+      if (pr >= 0 && pr < src_rows) val = s[static_cast<int64_t>(pr) * vpr + c];
+    }
+    d[idx] = val;
+  }
+}
+
+template <typename V>
+__global__ void __launch_bounds__(256) scatter_rows_kernel(
+    const V* __restrict__ src, const int32_t* __restrict__ perm, V* __restrict__ dst,
+    int64_t src_rows, int n_perm, int64_t dst_rows, int vpr) {
+  const int64_t h = blockIdx.y;
+  const V* s = src + h * src_rows * vpr;
+  V* d = dst + h * dst_rows * vpr;
+  const int total = n_perm * vpr;
+  for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += gridDim.x * blockDim.x) {
+    const int r = idx / vpr;
+    const int c = idx - r * vpr;
+    const int pr = perm[r];
+    if (pr >= 0 && pr < dst_rows) d[static_cast<int64_t>(pr) * vpr + c] = s[idx];
+  }
+}
+
+template <typename V>
+int launch_rows(bool scatter, const void* src, const int32_t* perm, void* dst,
+                int64_t heads, int64_t src_rows, int64_t n_perm, int64_t dst_rows,
+                int vpr, hipStream_t stream) {
+  const int64_t work = (scatter ? n_perm : dst_rows) * vpr;
+  const int64_t blocks = (work + 255) / 256;
+  dim3 grid(static_cast<unsigned>(blocks < 2048 ? (blocks > 0 ? blocks : 1) : 2048),
+            static_cast<unsigned>(heads));
+  if (scatter)
+    scatter_rows_kernel<V><<<grid, 256, 0, stream>>>(
+        static_cast<const V*>(src), perm, static_cast<V*>(dst), src_rows,
+        static_cast<int>(n_perm), dst_rows, vpr);
+  else
+    gather_rows_kernel<V><<<grid, 256, 0, stream>>>(
+        static_cast<const V*>(src), perm, static_cast<V*>(dst), src_rows,
+        static_cast<int>(n_perm), static_cast<int>(dst_rows), vpr);
+  return check_launch(scatter ? "dfs_permute_scatter" : "dfs_permute_gather");
+}
+
+int permute_rows(bool scatter, const void* src, const int32_t* perm, void* dst,
+                 int64_t heads, int64_t src_rows, int64_t n_perm, int64_t dst_rows,
+                 int64_t row_bytes, hipStream_t stream) {
+  const char* name = scatter ? "dfs_permute_scatter" : "dfs_permute_gather";
+  DFS_REQUIRE(src && perm && dst, "%s: NULL pointer", name);
+  DFS_REQUIRE(heads > 0 && heads < 65536, "%s: heads=%lld out of range", name, (long long)heads);
+  DFS_REQUIRE(row_bytes > 0 && row_bytes % 2 == 0, "%s: row_bytes=%lld must be a positive even number",
+              name, (long long)row_bytes);
+  DFS_REQUIRE(n_perm >= 0 && src_rows >= 0 && dst_rows >= 0, "%s: negative size", name);
+  DFS_REQUIRE(scatter ? n_perm <= src_rows : n_perm <= dst_rows,
+              "%s: n_perm=%lld exceeds the permuted tensor's rows", name, (long long)n_perm);
+  const int64_t rows = scatter ? n_perm : dst_rows;
+  DFS_REQUIRE(rows * row_bytes / 2 < (int64_t(1) << 31),
+              "%s: %lld rows x %lld bytes per head exceeds the 32-bit per-head index range",
+              name, (long long)rows, (long long)row_bytes);
+  if (rows == 0) return 0;
+  if (row_bytes % 16 == 0)
+    return launch_rows<uint4>(scatter, src, perm, dst, heads, src_rows, n_perm, dst_rows,
+                              static_cast<int>(row_bytes / 16), stream);
+  if (row_bytes % 4 == 0)
+    return launch_rows<uint32_t>(scatter, src, perm, dst, heads, src_rows, n_perm, dst_rows,
+                                 static_cast<int>(row_bytes / 4), stream);
+  return launch_rows<uint16_t>(scatter, src, perm, dst, heads, src_rows, n_perm, dst_rows,
+                               static_cast<int>(row_bytes / 2), stream);
+}
+
+struct PrepParams {
+  const uint4* q;  // [H][L][D] as 16-byte chunks
+  const uint4* k;
+  const uint4* v;
+  const int32_t* perm;
+  uint4* q_perm;  // [H][R][D]
+  uint4* k_perm;
+  uint4* v_t;  // [H][R/128][D][128]
+  uint4* q_hi;  // [H][q_tiles][D] bf16
+  uint4* q_lo;
+  uint4* k_hi;  // [H][k_tiles][D] bf16
+  uint4* k_lo;
+  int32_t* v_overflow;
+  int L;         // tokens
+  int Lv;        // video tokens (== L for Wan)
+  int R;         // execution rows per head, ceil(L/128)*128
+  int vpad;      // zero rows inserted after the video in the scoring layout
+  int q_tiles;   // pooled query tiles (video part of the scoring layout)
+  int k_tiles;   // pooled key tiles (whole scoring layout)
+  int tile;      // tokens per tile
+  int in_f16;    // q/k/v are f16 (else bf16)
+  int pv_convert;  // v_t receives bf16 -> f16 converted values
+  int pool;      // write pooled tiles
+};
+
+// Scoring-layout position -> execution row, or -1 for an inserted zero row.
+__device__ __forceinline__ int scoring_to_exec(int pos, const PrepParams& p) {
+  if (pos < p.Lv) return pos;
+  if (pos < p.Lv + p.vpad) return -1;
+  const int x = pos - p.vpad;
+  return x < p.L ? x : -1;
+}
+
+__device__ __forceinline__ void add_chunk(float acc[8], const uint4& v, bool f16) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    acc[i] += f16 ? f16_bits_to_f32(u16_at(v, i)) : bf16_bits_to_f32(u16_at(v, i));
+}
+
+// One wave per (tensor, head, scoring tile): gathers the tile's rows into the
+// execution layout and writes the tile mean as a bf16 hi/lo pair. Zero rows of
+// the scoring layout count toward the mean, as in the reference's zero-padded
+// .view(...).mean(3). Tiles past the query tiles still gather text rows of Q.
+template <int D>
+__global__ void __launch_bounds__(256) prep_qk_kernel(PrepParams p) {
+  constexpr int CPR = D / 8;        // 16-byte chunks per row
+  constexpr int RPP = kWave / CPR;  // rows covered per pass
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int h = blockIdx.y;
+  const bool is_k = blockIdx.z == 1;
+  const uint4* src = (is_k ? p.k : p.q) + static_cast<int64_t>(h) * p.L * CPR;
+  uint4* dst = (is_k ? p.k_perm : p.q_perm) + static_cast<int64_t>(h) * p.R * CPR;
+
+  // Zero-fill execution rows L..R-1 (done by the last block of each tensor/head).
+  if (blockIdx.x == gridDim.x - 1) {
+    const int n = (p.R - p.L) * CPR;
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
+      dst[static_cast<int64_t>(p.L) * CPR + i] = make_uint4(0, 0, 0, 0);
+  }
+
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= p.k_tiles) return;
+  const int c = lane % CPR;
+  const int g = lane / CPR;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int r = g; r < p.tile; r += RPP) {
+    const int x = scoring_to_exec(t * p.tile + r, p);
+    if (x >= 0) {
+      const int s = p.perm[x];
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (s >= 0 && s < p.L) val = src[static_cast<int64_t>(s) * CPR + c];
+      dst[static_cast<int64_t>(x) * CPR + c] = val;
+      add_chunk(acc, val, p.in_f16 != 0);
+    }
+  }
+  const int n_tiles = is_k ? p.k_tiles : p.q_tiles;
+  if (!p.pool || t >= n_tiles) return;
+#pragma unroll
+  for (int off = CPR; off < kWave; off <<= 1)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += __shfl_xor(acc[i], off);
+  if (g != 0) return;
+  const float inv = 1.0f / static_cast<float>(p.tile);
+  uint32_t hi[8], lo[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float mean = acc[i] * inv;
+    hi[i] = f32_to_bf16_bits(mean);
+    lo[i] = f32_to_bf16_bits(mean - bf16_bits_to_f32(hi[i]));
+  }
+  const int64_t o = (static_cast<int64_t>(h) * n_tiles + t) * CPR + c;
+  (is_k ? p.k_hi : p.q_hi)[o] = make_uint4(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16),
+                                           hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16));
+  (is_k ? p.k_lo : p.q_lo)[o] = make_uint4(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
+                                           lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16));
+}
+
+// Inside every 16-token group of v_t, physical slot s holds token swap23(s):
+// bits 2 and 3 exchanged. Lane half j of the PV MFMA then reads its eight
+// tokens {4j..4j+3, 8+4j..8+4j+3} as one contiguous 16-byte vector, matching
+// the register order of the S^T accumulator it is multiplied with.
+__device__ __forceinline__ int swap23(int s) {
+  return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1);
+}
+
+// One block per (128-token block, head): gathers 128 V rows (zero past L),
+// transposes them to [D][128] in 8x8 register tiles, optionally converting
+// bf16 to f16.
+template <int D>
+__global__ void __launch_bounds__(16 * (D / 8)) prep_v_kernel(PrepParams p) {
+  constexpr int CPR = D / 8;
+  const int kb = blockIdx.x;
+  const int h = blockIdx.y;
+  const int dg = threadIdx.x % CPR;   // 8 head dims: dg*8 .. dg*8+7
+  const int kg = threadIdx.x / CPR;   // 8 physical token slots: kg*8 .. kg*8+7
+  const uint4* src = p.v + static_cast<int64_t>(h) * p.L * CPR;
+  uint4 rows[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int phys = kg * 8 + i;
+    const int tok = kb * kBlock + (phys & ~15) + swap23(phys & 15);
+    rows[i] = make_uint4(0, 0, 0, 0);
+    if (tok < p.L) {
+      const int s = p.perm[tok];
+      if (s >= 0 && s < p.L) rows[i] = src[static_cast<int64_t>(s) * CPR + dg];
+    }
+  }
+  bool overflow = false;
+  uint4* dst = p.v_t + (static_cast<int64_t>(h) * (p.R / kBlock) + kb) * D * (kBlock / 8);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint32_t e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t bits = u16_at(rows[i], j);
+      if (p.pv_convert) {
+        const float f = bf16_bits_to_f32(bits);
+        bits = f32_to_f16_bits(f);
+        overflow |= ((bits & 0x7fffu) == 0x7c00u) && !isinf(f);  // finite -> inf
+      }
+      e[i] = bits;
+    }
+    const int d = dg * 8 + j;
+    dst[d * (kBlock / 8) + kg] =
+        make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+  }
+  if (p.v_overflow && overflow) atomicOr(p.v_overflow, 1);
+}
+
+}  // namespace
+}  // namespace dfs
+
+extern "C" {
+
+int dfs_permute_gather(const void* src, const int32_t* perm, void* dst, int64_t heads,
+                       int64_t src_rows, int64_t n_perm, int64_t dst_rows, int64_t row_bytes,
+                       dfs_stream_t stream) {
+  return dfs::permute_rows(false, src, perm, dst, heads, src_rows, n_perm, dst_rows, row_bytes,
+                           reinterpret_cast<hipStream_t>(stream));
+}
+
+int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst, int64_t heads,
+                        int64_t src_rows, int64_t n_perm, int64_t dst_rows, int64_t row_bytes,
+                        dfs_stream_t stream) {
+  return dfs::permute_rows(true, src, perm, dst, heads, src_rows, n_perm, dst_rows, row_bytes,
+                           reinterpret_cast<hipStream_t>(stream));
+}
+
+int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* perm,
+                    int64_t heads, int64_t seq_len, int64_t head_dim, int dtype,
+                    int64_t video_len, int64_t tile_size, int pv_dtype, void* q_perm,
+                    void* k_perm, void* v_t, uint16_t* q_pool_hi, uint16_t* q_pool_lo,
+                    uint16_t* k_pool_hi, uint16_t* k_pool_lo, int32_t* v_overflow,
+                    dfs_stream_t stream) {
+  using namespace dfs;
+  DFS_REQUIRE(q && k && v && perm && q_perm && k_perm && v_t, "dfs_prepare_qkv: NULL operand");
+  DFS_REQUIRE(head_dim == 64 || head_dim == 128, "dfs_prepare_qkv: head_dim=%lld (supported: 64, 128)",
+              (long long)head_dim);
+  DFS_REQUIRE(dtype == DFS_DTYPE_BF16 || dtype == DFS_DTYPE_F16,
+              "dfs_prepare_qkv: dtype=%d (supported: bf16, f16)", dtype);
+  DFS_REQUIRE(pv_dtype == DFS_DTYPE_BF16 || pv_dtype == DFS_DTYPE_F16,
+              "dfs_prepare_qkv: pv_dtype=%d (supported: bf16, f16)", pv_dtype);
+  DFS_REQUIRE(!(dtype == DFS_DTYPE_F16 && pv_dtype == DFS_DTYPE_BF16),
+              "dfs_prepare_qkv: f16 inputs need an f16 PV operand");
+  DFS_REQUIRE(heads > 0 && heads < 65536, "dfs_prepare_qkv: heads=%lld out of range", (long long)heads);
+  DFS_REQUIRE(seq_len > 0 && video_len > 0 && video_len <= seq_len,
+              "dfs_prepare_qkv: need 0 < video_len=%lld <= seq_len=%lld", (long long)video_len,
+              (long long)seq_len);
+  DFS_REQUIRE(tile_size > 0 && kBlock % tile_size == 0,
+              "dfs_prepare_qkv: tile_size=%lld must divide 128", (long long)tile_size);
+  const int64_t kb = (seq_len + kBlock - 1) / kBlock;
+  const int64_t vb = (video_len + kBlock - 1) / kBlock;
+  const int64_t vpad = vb * kBlock - video_len;
+  DFS_REQUIRE(video_len + vpad + (seq_len - video_len) <= kb * kBlock,
+              "dfs_prepare_qkv: padded scoring layout (%lld tokens) exceeds %lld blocks; the "
+              "reference's tile view fails for this video/text split",
+              (long long)(video_len + vpad + (seq_len - video_len)), (long long)kb);
+  DFS_REQUIRE(kb * kBlock * head_dim < (int64_t(1) << 31),
+              "dfs_prepare_qkv: seq_len=%lld too long for 32-bit per-head indexing", (long long)seq_len);
+  const bool pool = q_pool_hi || q_pool_lo || k_pool_hi || k_pool_lo;
+  DFS_REQUIRE(!pool || (q_pool_hi && q_pool_lo && k_pool_hi && k_pool_lo),
+              "dfs_prepare_qkv: pooled outputs must be all set or all NULL");
+
+  PrepParams p{};
+  p.q = static_cast<const uint4*>(q);
+  p.k = static_cast<const uint4*>(k);
+  p.v = static_cast<const uint4*>(v);
+  p.perm = perm;
+  p.q_perm = static_cast<uint4*>(q_perm);
+  p.k_perm = static_cast<uint4*>(k_perm);
+  p.v_t = static_cast<uint4*>(v_t);
+  p.q_hi = reinterpret_cast<uint4*>(q_pool_hi);
+  p.q_lo = reinterpret_cast<uint4*>(q_pool_lo);
+  p.k_hi = reinterpret_cast<uint4*>(k_pool_hi);
+  p.k_lo = reinterpret_cast<uint4*>(k_pool_lo);
+  p.v_overflow = v_overflow;
+  p.L = static_cast<int>(seq_len);
+  p.Lv = static_cast<int>(video_len);
+  p.R = static_cast<int>(kb * kBlock);
+  p.vpad = static_cast<int>(vpad);
+  p.tile = static_cast<int>(tile_size);
+  p.q_tiles = static_cast<int>(vb * kBlock / tile_size);
+  p.k_tiles = static_cast<int>(kb * kBlock / tile_size);
+  p.in_f16 = dtype == DFS_DTYPE_F16;
+  p.pv_convert = (dtype == DFS_DTYPE_BF16 && pv_dtype == DFS_DTYPE_F16);
+  p.pool = pool ? 1 : 0;
+
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 gqk(static_cast<unsigned>((p.k_tiles + 3) / 4), static_cast<unsigned>(heads), 2);
+  dim3 gv(static_cast<unsigned>(kb), static_cast<unsigned>(heads));
+  if (head_dim == 128) {
+    prep_qk_kernel<128><<<gqk, 256, 0, s>>>(p);
+    prep_v_kernel<128><<<gv, 16 * 16, 0, s>>>(p);
+  } else {
+    prep_qk_kernel<64><<<gqk, 256, 0, s>>>(p);
+    prep_v_kernel<64><<<gv, 16 * 8, 0, s>>>(p);
+  }
+  return check_launch("dfs_prepare_qkv");
+}
+
+}  // extern "C"

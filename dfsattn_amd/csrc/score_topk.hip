@@ -1,0 +1,411 @@
+// Hierarchical block scoring and per-row top-k block selection.
+//
+// Scoring (reference: dfsattn/attention_wan.py:157-253 and
+// dfsattn/attention_hyvideo.py:310-501): with pooled tile means q_i, k_j,
+//   P[i, j]      = softmax_j( q_i . k_j * D^-1/2 )   over ALL key tiles j
+//   score[a, b]  = sum_{i in query block a} sum_{j in key block b} P[i, j]
+// followed by a top-k over each row a. One workgroup owns 32 query tiles of one
+// head; its four waves stream the pooled key tiles in 32-tile chunks through
+// bf16 MFMAs on a hi/lo split (q.k ~= qh.kh + qh.kl + ql.kh, relative error
+// ~2^-16), so the scores track the fp32 computation closely. Pass 1 builds the
+// per-tile softmax max / normaliser, pass 2 accumulates block sums in LDS, and
+// the same workgroup then selects the top-k of every row it owns, one wave per
+// row, emitting CSR column indices for the attention kernel.
+#include <math.h>
+
+#include "common.h"
+
+namespace dfs {
+namespace {
+
+__device__ __forceinline__ void lds_sync_wave() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Order-preserving map of an fp32 score to uint32 (NaN sorts above +inf, as in
+// torch.topk).
+__device__ __forceinline__ uint32_t order_key(float s) {
+  const uint32_t u = __float_as_uint(s);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t lanes_below(int lane) {
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Selection of one mask row by one wave.
+//  * columns [0, n_cand): the k_pick largest scores, ties broken by lower
+//    column first (radix select on the order keys, 4 x 8-bit digits);
+//  * columns [n_cand, dense_col): never kept;
+//  * columns [dense_col, kb): always kept.
+// cols receives the kept columns in ascending order; mask_row (optional) the
+// uint8 mask. hist is 256 words of wave-private LDS.
+__device__ void select_row(const float* scores, int n_cand, int k_pick, int dense_col, int kb,
+                           int32_t* cols, uint8_t* mask_row, uint32_t* hist, int lane) {
+  uint32_t prefix = 0, pmask = 0;
+  int remaining = k_pick;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int b = lane; b < 256; b += kWave) hist[b] = 0;
+    lds_sync_wave();
+    for (int j = lane; j < n_cand; j += kWave) {
+      const uint32_t key = order_key(scores[j]);
+      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    lds_sync_wave();
+    // Lane i owns digits 255-4i .. 252-4i, highest first.
+    uint32_t c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = hist[255 - 4 * lane - i];
+    const uint32_t own = c[0] + c[1] + c[2] + c[3];
+    uint32_t incl = own;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t o = __shfl_up(incl, off);
+      if (lane >= off) incl += o;
+    }
+    const uint32_t excl = incl - own;
+    const bool mine = excl < static_cast<uint32_t>(remaining) &&
+                      static_cast<uint32_t>(remaining) <= incl;
+    int pick = 0;
+    uint32_t above = excl;
+    if (mine) {
+      while (above + c[pick] < static_cast<uint32_t>(remaining)) above += c[pick++];
+    }
+    const uint64_t who = __ballot(mine);
+    const int src = __ffsll(static_cast<unsigned long long>(who)) - 1;
+    const int digit = __shfl(255 - 4 * lane - pick, src);
+    const uint32_t above_d = __shfl(above, src);
+    prefix |= static_cast<uint32_t>(digit) << shift;
+    pmask |= 255u << shift;
+    remaining -= static_cast<int>(above_d);
+  }
+  // prefix is the order key of the k-th largest score; `remaining` of the
+  // candidates equal to it are kept, lowest column first.
+  const uint64_t below = lanes_below(lane);
+  int out = 0, ties = 0;
+  for (int base = 0; base < n_cand; base += kWave) {
+    const int j = base + lane;
+    const bool valid = j < n_cand;
+    const uint32_t key = valid ? order_key(scores[j]) : 0u;
+    const bool eq = valid && key == prefix;
+    const uint64_t eqb = __ballot(eq);
+    const bool take = (valid && key > prefix) ||
+                      (eq && ties + __popcll(eqb & below) < remaining);
+    const uint64_t tb = __ballot(take);
+    if (take) cols[out + __popcll(tb & below)] = j;
+    if (mask_row && valid) mask_row[j] = take ? 1 : 0;
+    out += __popcll(tb);
+    ties += __popcll(eqb);
+  }
+  if (mask_row)
+    for (int j = n_cand + lane; j < dense_col; j += kWave) mask_row[j] = 0;
+  for (int j = dense_col + lane; j < kb; j += kWave) {
+    cols[out + (j - dense_col)] = j;
+    if (mask_row) mask_row[j] = 1;
+  }
+}
+
+__device__ void dense_row(int kb, int32_t* cols, uint8_t* mask_row, int lane) {
+  for (int j = lane; j < kb; j += kWave) {
+    cols[j] = j;
+    if (mask_row) mask_row[j] = 1;
+  }
+}
+
+struct Policy {
+  int Qb, Kb, scored_rows, n_cand, k_pick, dense_col, dense_row;
+};
+
+struct ScoreParams {
+  const uint4* q_hi;  // [H][q_tiles][D] bf16
+  const uint4* q_lo;
+  const uint4* k_hi;  // [H][k_tiles][D] bf16
+  const uint4* k_lo;
+  const int32_t* row_ptr;
+  int32_t* col_idx;
+  float* scores_out;
+  uint8_t* mask_out;
+  Policy pol;
+  int q_tiles, k_tiles;
+  float scale_log2;
+};
+
+// S^T chunk (32 key tiles x 32 query tiles) on the hi/lo split.
+template <int D>
+__device__ __forceinline__ f32x16 score_chunk(const ScoreParams& p, int h, int chunk, int l32,
+                                              int hl, const bf16x8* qh, const bf16x8* ql) {
+  constexpr int CPR = D / 8;
+  f32x16 acc = {};
+  const int kt = chunk * 32 + l32;
+  const bool valid = kt < p.k_tiles;
+  const int64_t base = (static_cast<int64_t>(h) * p.k_tiles + (valid ? kt : 0)) * CPR + hl;
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) {
+    uint4 a_hi = valid ? p.k_hi[base + 2 * ds] : make_uint4(0, 0, 0, 0);
+    uint4 a_lo = valid ? p.k_lo[base + 2 * ds] : make_uint4(0, 0, 0, 0);
+    const bf16x8 kh = __builtin_bit_cast(bf16x8, a_hi);
+    const bf16x8 kl = __builtin_bit_cast(bf16x8, a_lo);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[ds], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[ds], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[ds], acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// Key-tile row held in accumulator register r by lane half hl (32x32 MFMA
+// output layout).
+__device__ __forceinline__ int acc_row(int r, int hl) { return (r >> 2) * 8 + hl * 4 + (r & 3); }
+
+template <int D, int TPB>
+__global__ void __launch_bounds__(256) score_topk_kernel(ScoreParams p) {
+  constexpr int CPR = D / 8;
+  constexpr int G = 32 / TPB;  // query blocks per workgroup
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const Policy& pol = p.pol;
+  float* bsum = smem;                           // [G][Kb]
+  float* st_m = bsum + G * pol.Kb;              // [4][2][32]
+  float* st_z = st_m + 256;                     // [4][2][32]
+  uint32_t* hist = reinterpret_cast<uint32_t*>(st_z + 256);  // [4][256]
+
+  const int h = blockIdx.y;
+  const int qb0 = blockIdx.x * G;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int score_rows = min(pol.scored_rows, pol.dense_row);
+  const bool do_score = qb0 < score_rows;
+
+  if (do_score) {
+    // Query fragments: lane column = query tile, 8 dims per lane half.
+    bf16x8 qh[D / 16], ql[D / 16];
+    const int qt = qb0 * TPB + l32;
+    const bool qv = qt < p.q_tiles;
+    const int64_t qbase = (static_cast<int64_t>(h) * p.q_tiles + (qv ? qt : 0)) * CPR + hl;
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ++ds) {
+      qh[ds] = __builtin_bit_cast(bf16x8, qv ? p.q_hi[qbase + 2 * ds] : make_uint4(0, 0, 0, 0));
+      ql[ds] = __builtin_bit_cast(bf16x8, qv ? p.q_lo[qbase + 2 * ds] : make_uint4(0, 0, 0, 0));
+    }
+    const int nchunks = (p.k_tiles + 31) / 32;
+
+    // Pass 1: running max and normaliser (log2 domain) of every query tile.
+    float m = -INFINITY, z = 0.f;
+    for (int c = w; c < nchunks; c += 4) {
+      const f32x16 acc = score_chunk<D>(p, h, c, l32, hl, qh, ql);
+      float t[16];
+      float cm = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool kv = c * 32 + acc_row(r, hl) < p.k_tiles;
+        t[r] = kv ? acc[r] * p.scale_log2 : -INFINITY;
+        cm = fmaxf(cm, t[r]);
+      }
+      const float mn = fmaxf(m, cm);
+      if (mn > -INFINITY) {
+        float s = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += exp2_fast(t[r] - mn);
+        z = (m > -INFINITY ? z * exp2_fast(m - mn) : 0.f) + s;
+        m = mn;
+      }
+    }
+    st_m[(w * 2 + hl) * 32 + l32] = m;
+    st_z[(w * 2 + hl) * 32 + l32] = z;
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) M = fmaxf(M, st_m[e * 32 + l32]);
+    float Z = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float me = st_m[e * 32 + l32];
+      if (me > -INFINITY) Z += st_z[e * 32 + l32] * exp2_fast(me - M);
+    }
+    const float invZ = Z > 0.f ? 1.0f / Z : 0.f;
+
+    // Pass 2: tile probabilities summed into 128x128 blocks.
+    for (int c = w; c < nchunks; c += 4) {
+      const f32x16 acc = score_chunk<D>(p, h, c, l32, hl, qh, ql);
+      float pr[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool kv = c * 32 + acc_row(r, hl) < p.k_tiles;
+        pr[r] = kv ? exp2_fast(acc[r] * p.scale_log2 - M) * invZ : 0.f;
+      }
+      if constexpr (TPB == 8) {
+        // Register group r/4 = key block b of the chunk; halves hold the
+        // other four tiles; 8 lanes = the 8 query tiles of a block.
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          float s = (pr[4 * b] + pr[4 * b + 1]) + (pr[4 * b + 2] + pr[4 * b + 3]);
+          s += __shfl_xor(s, 32);
+          s += __shfl_xor(s, 1);
+          s += __shfl_xor(s, 2);
+          s += __shfl_xor(s, 4);
+          const int kbk = c * 4 + b;
+          if (hl == 0 && (l32 & 7) == 0 && kbk < pol.Kb) bsum[(l32 >> 3) * pol.Kb + kbk] = s;
+        }
+      } else {
+        // TPB == 4: register group gg and half hl form key block 2*gg + hl.
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+          float s = (pr[4 * gg] + pr[4 * gg + 1]) + (pr[4 * gg + 2] + pr[4 * gg + 3]);
+          s += __shfl_xor(s, 1);
+          s += __shfl_xor(s, 2);
+          const int kbk = c * 8 + 2 * gg + hl;
+          if ((l32 & 3) == 0 && kbk < pol.Kb) bsum[(l32 >> 2) * pol.Kb + kbk] = s;
+        }
+      }
+    }
+    __syncthreads();
+    if (p.scores_out) {
+      for (int i = tid; i < G * pol.Kb; i += 256) {
+        const int g = i / pol.Kb, col = i - g * pol.Kb;
+        const int qb = qb0 + g;
+        if (qb < pol.scored_rows)
+          p.scores_out[(static_cast<int64_t>(h) * pol.scored_rows + qb) * pol.Kb + col] = bsum[i];
+      }
+    }
+  }
+
+  for (int g = w; g < G; g += 4) {
+    const int qb = qb0 + g;
+    if (qb >= pol.Qb) break;
+    const int64_t row = static_cast<int64_t>(h) * pol.Qb + qb;
+    int32_t* cols = p.col_idx + p.row_ptr[row];
+    uint8_t* mrow = p.mask_out ? p.mask_out + row * pol.Kb : nullptr;
+    if (qb >= pol.dense_row || qb >= pol.scored_rows)
+      dense_row(pol.Kb, cols, mrow, lane);
+    else
+      select_row(bsum + g * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow,
+                 hist + w * 256, lane);
+  }
+}
+
+struct TopkParams {
+  const float* scores;  // [H][scored_rows][Kb]
+  const int32_t* row_ptr;
+  int32_t* col_idx;
+  uint8_t* mask_out;
+  Policy pol;
+  int heads;
+};
+
+__global__ void __launch_bounds__(256) topk_rows_kernel(TopkParams p) {
+  __shared__ uint32_t hist[4][256];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  const Policy& pol = p.pol;
+  if (row >= static_cast<int64_t>(p.heads) * pol.Qb) return;
+  const int h = static_cast<int>(row / pol.Qb), qb = static_cast<int>(row % pol.Qb);
+  int32_t* cols = p.col_idx + p.row_ptr[row];
+  uint8_t* mrow = p.mask_out ? p.mask_out + row * pol.Kb : nullptr;
+  if (qb >= pol.dense_row || qb >= pol.scored_rows) {
+    dense_row(pol.Kb, cols, mrow, lane);
+    return;
+  }
+  const float* srow = p.scores + (static_cast<int64_t>(h) * pol.scored_rows + qb) * pol.Kb;
+  select_row(srow, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow, hist[w], lane);
+}
+
+int check_policy(const char* name, int64_t heads, int64_t q_blocks, int64_t k_blocks,
+                 int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
+                 int64_t dense_row_start) {
+  DFS_REQUIRE(heads > 0 && heads < 65536, "%s: heads=%lld out of range", name, (long long)heads);
+  DFS_REQUIRE(q_blocks > 0 && k_blocks > 0 && q_blocks < (1 << 20) && k_blocks < (1 << 20),
+              "%s: q_blocks=%lld / k_blocks=%lld out of range", name, (long long)q_blocks,
+              (long long)k_blocks);
+  DFS_REQUIRE(scored_rows >= 0 && scored_rows <= q_blocks, "%s: scored_rows=%lld not in [0, %lld]",
+              name, (long long)scored_rows, (long long)q_blocks);
+  DFS_REQUIRE(dense_row_start >= 0 && dense_row_start <= scored_rows,
+              "%s: dense_row=%lld must not exceed scored_rows=%lld", name,
+              (long long)dense_row_start, (long long)scored_rows);
+  DFS_REQUIRE(n_cand >= 0 && n_cand <= dense_col && dense_col <= k_blocks,
+              "%s: need 0 <= n_cand=%lld <= dense_col=%lld <= k_blocks=%lld", name,
+              (long long)n_cand, (long long)dense_col, (long long)k_blocks);
+  DFS_REQUIRE(dense_row_start == 0 || (k_pick >= 1 && k_pick <= n_cand),
+              "%s: k_pick=%lld must be in [1, n_cand=%lld] (torch.topk: selected index k out of range)",
+              name, (long long)k_pick, (long long)n_cand);
+  return 0;
+}
+
+}  // namespace
+}  // namespace dfs
+
+extern "C" {
+
+int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
+                         const uint16_t* k_pool_hi, const uint16_t* k_pool_lo, int64_t heads,
+                         int64_t head_dim, int64_t tile_size, int64_t q_blocks, int64_t k_blocks,
+                         int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
+                         int64_t dense_row, const int32_t* row_ptr, int32_t* col_idx,
+                         float* scores_out, uint8_t* mask_out, dfs_stream_t stream) {
+  using namespace dfs;
+  const char* name = "dfs_block_score_topk";
+  DFS_REQUIRE(q_pool_hi && q_pool_lo && k_pool_hi && k_pool_lo && row_ptr && col_idx,
+              "%s: NULL operand", name);
+  DFS_REQUIRE(head_dim == 64 || head_dim == 128, "%s: head_dim=%lld (supported: 64, 128)", name,
+              (long long)head_dim);
+  DFS_REQUIRE(tile_size == 16 || tile_size == 32, "%s: tile_size=%lld (supported: 16, 32)", name,
+              (long long)tile_size);
+  if (int rc = check_policy(name, heads, q_blocks, k_blocks, scored_rows, n_cand, k_pick,
+                            dense_col, dense_row))
+    return rc;
+  const int tpb = static_cast<int>(kBlock / tile_size);
+  const int G = 32 / tpb;
+  const size_t smem = (static_cast<size_t>(G) * k_blocks + 512) * sizeof(float) + 4 * 256 * 4;
+  DFS_REQUIRE(smem <= 160 * 1024, "%s: k_blocks=%lld needs %zu bytes of LDS (max 163840)", name,
+              (long long)k_blocks, smem);
+  ScoreParams p{};
+  p.q_hi = reinterpret_cast<const uint4*>(q_pool_hi);
+  p.q_lo = reinterpret_cast<const uint4*>(q_pool_lo);
+  p.k_hi = reinterpret_cast<const uint4*>(k_pool_hi);
+  p.k_lo = reinterpret_cast<const uint4*>(k_pool_lo);
+  p.row_ptr = row_ptr;
+  p.col_idx = col_idx;
+  p.scores_out = scores_out;
+  p.mask_out = mask_out;
+  p.pol = Policy{static_cast<int>(q_blocks), static_cast<int>(k_blocks), static_cast<int>(scored_rows),
+                 static_cast<int>(n_cand), static_cast<int>(k_pick), static_cast<int>(dense_col),
+                 static_cast<int>(dense_row)};
+  p.q_tiles = static_cast<int>(scored_rows * tpb);
+  p.k_tiles = static_cast<int>(k_blocks * tpb);
+  p.scale_log2 = static_cast<float>(1.4426950408889634 / sqrt(static_cast<double>(head_dim)));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>((q_blocks + G - 1) / G), static_cast<unsigned>(heads));
+  if (head_dim == 128 && tpb == 8)
+    score_topk_kernel<128, 8><<<grid, 256, smem, s>>>(p);
+  else if (head_dim == 128)
+    score_topk_kernel<128, 4><<<grid, 256, smem, s>>>(p);
+  else if (tpb == 8)
+    score_topk_kernel<64, 8><<<grid, 256, smem, s>>>(p);
+  else
+    score_topk_kernel<64, 4><<<grid, 256, smem, s>>>(p);
+  return check_launch(name);
+}
+
+int dfs_topk_from_scores(const float* scores, int64_t heads, int64_t q_blocks, int64_t k_blocks,
+                         int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
+                         int64_t dense_row, const int32_t* row_ptr, int32_t* col_idx,
+                         uint8_t* mask_out, dfs_stream_t stream) {
+  using namespace dfs;
+  const char* name = "dfs_topk_from_scores";
+  DFS_REQUIRE(scores && row_ptr && col_idx, "%s: NULL operand", name);
+  if (int rc = check_policy(name, heads, q_blocks, k_blocks, scored_rows, n_cand, k_pick,
+                            dense_col, dense_row))
+    return rc;
+  TopkParams p{};
+  p.scores = scores;
+  p.row_ptr = row_ptr;
+  p.col_idx = col_idx;
+  p.mask_out = mask_out;
+  p.pol = Policy{static_cast<int>(q_blocks), static_cast<int>(k_blocks), static_cast<int>(scored_rows),
+                 static_cast<int>(n_cand), static_cast<int>(k_pick), static_cast<int>(dense_col),
+                 static_cast<int>(dense_row)};
+  p.heads = static_cast<int>(heads);
+  const int64_t rows = heads * q_blocks;
+  topk_rows_kernel<<<static_cast<unsigned>((rows + 3) / 4), 256, 0,
+                     reinterpret_cast<hipStream_t>(stream)>>>(p);
+  return check_launch(name);
+}
+
+}  // extern "C"

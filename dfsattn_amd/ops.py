@@ -1,0 +1,243 @@
+"""Device operations of the DFS hot path: thin wrappers over the C-ABI.
+
+torch supplies device memory and the current stream; every computation runs
+in the HIP kernels of libdfsattn_amd.so. Tensors must live on a ROCm device —
+there is deliberately no CPU path here.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from .layout import ScoringLayout, TopkPolicy
+
+DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_device(*tensors: Optional[torch.Tensor]) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                "DFS kernels run on a ROCm GPU only; got a tensor on " + str(t.device))
+
+
+def _heads_rows(x: torch.Tensor) -> Tuple[int, int, int]:
+    if x.dim() == 4:
+        if x.shape[0] != 1:
+            raise AssertionError("DFS Attention with block sparse currently supports batch size 1.")
+        return x.shape[1], x.shape[2], x.shape[3]
+    if x.dim() == 3:
+        return x.shape[0], x.shape[1], x.shape[2]
+    raise ValueError(f"expected [1,H,L,D] or [H,L,D], got {tuple(x.shape)}")
+
+
+def device_perm(perm: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """int32 copy of a permutation on the device (validated on the host)."""
+    p = torch.as_tensor(perm)
+    if p.dim() != 1:
+        raise ValueError("permutation must be 1-D")
+    if p.device.type == "cpu":
+        n = p.numel()
+        if n and (int(p.min()) < 0 or int(p.max()) >= n or torch.unique(p).numel() != n):
+            raise ValueError("video_perm is not a permutation of range(len)")
+    return p.to(device=device, dtype=torch.int32).contiguous()
+
+
+def permute_gather(src: torch.Tensor, perm: torch.Tensor, rows: Optional[int] = None) -> torch.Tensor:
+    """out[..., i, :] = src[..., perm[i], :] (rows >= len(perm) zero)."""
+    _require_device(src, perm)
+    heads, length, dim = _heads_rows(src)
+    src = src.contiguous()
+    n = perm.numel()
+    rows = n if rows is None else rows
+    out = torch.empty((*src.shape[:-2], rows, dim), dtype=src.dtype, device=src.device)
+    _lib.call("dfs_permute_gather", _ptr(src), _ptr(perm), _ptr(out), heads, length, n, rows,
+              dim * src.element_size(), _stream(src))
+    return out
+
+
+def permute_scatter(src: torch.Tensor, perm: torch.Tensor, out: Optional[torch.Tensor] = None,
+                    rows: Optional[int] = None) -> torch.Tensor:
+    """out[..., perm[i], :] = src[..., i, :] for i < len(perm)."""
+    _require_device(src, perm, out)
+    heads, length, dim = _heads_rows(src)
+    src = src.contiguous()
+    n = perm.numel()
+    if out is None:
+        rows = n if rows is None else rows
+        out = torch.empty((*src.shape[:-2], rows, dim), dtype=src.dtype, device=src.device)
+    _, out_rows, _ = _heads_rows(out)
+    _lib.call("dfs_permute_scatter", _ptr(src), _ptr(perm), _ptr(out), heads, length, n, out_rows,
+              dim * src.element_size(), _stream(src))
+    return out
+
+
+@dataclass
+class Prepared:
+    """Operands of one DFS call in execution (permuted) order."""
+
+    layout: ScoringLayout
+    heads: int
+    head_dim: int
+    dtype: torch.dtype
+    pv_dtype: torch.dtype
+    q_perm: torch.Tensor  # [H, R, D]
+    k_perm: torch.Tensor  # [H, R, D]
+    v_t: torch.Tensor     # [H, R/128, D, 128]
+    q_hi: Optional[torch.Tensor] = None  # [H, q_tiles, D] bf16
+    q_lo: Optional[torch.Tensor] = None
+    k_hi: Optional[torch.Tensor] = None  # [H, k_tiles, D] bf16
+    k_lo: Optional[torch.Tensor] = None
+    v_overflow: Optional[torch.Tensor] = None
+
+
+def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.Tensor,
+                layout: ScoringLayout, pv_dtype: Optional[torch.dtype] = None, pool: bool = True,
+                check_overflow: bool = False) -> Prepared:
+    """Gathers Q, K, V into execution order (V block-transposed) and, with
+    ``pool``, writes the tile means used for scoring."""
+    _require_device(q, k, v, perm)
+    heads, length, dim = _heads_rows(q)
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("DFS native attention only supports fp16 and bf16 inputs")
+    if k.shape != q.shape or v.shape != q.shape or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k and v must share shape and dtype")
+    if length != layout.seq_len:
+        raise ValueError(f"sequence length {length} does not match the layout ({layout.seq_len})")
+    if perm.numel() != length:
+        raise ValueError(f"permutation has {perm.numel()} entries for {length} tokens")
+    pv_dtype = pv_dtype or torch.float16
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    dev = q.device
+    rows = layout.rows
+    prep = Prepared(
+        layout=layout, heads=heads, head_dim=dim, dtype=q.dtype, pv_dtype=pv_dtype,
+        q_perm=torch.empty((heads, rows, dim), dtype=q.dtype, device=dev),
+        k_perm=torch.empty((heads, rows, dim), dtype=q.dtype, device=dev),
+        v_t=torch.empty((heads, rows // 128, dim, 128), dtype=pv_dtype, device=dev),
+    )
+    if pool:
+        prep.q_hi = torch.empty((heads, layout.q_tiles, dim), dtype=torch.bfloat16, device=dev)
+        prep.q_lo = torch.empty_like(prep.q_hi)
+        prep.k_hi = torch.empty((heads, layout.k_tiles, dim), dtype=torch.bfloat16, device=dev)
+        prep.k_lo = torch.empty_like(prep.k_hi)
+    if check_overflow:
+        prep.v_overflow = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.call("dfs_prepare_qkv", _ptr(q), _ptr(k), _ptr(v), _ptr(perm), heads, length, dim,
+              DTYPE_CODE[q.dtype], layout.video_len, layout.tile, DTYPE_CODE[pv_dtype],
+              _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(prep.q_hi), _ptr(prep.q_lo),
+              _ptr(prep.k_hi), _ptr(prep.k_lo), _ptr(prep.v_overflow), _stream(q))
+    return prep
+
+
+def _policy_args(policy: TopkPolicy):
+    return (policy.q_blocks, policy.k_blocks, policy.scored_rows, policy.n_cand, policy.k_pick,
+            policy.dense_col, policy.dense_row)
+
+
+def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
+                     want_scores: bool = False, want_mask: bool = False):
+    """Scores + top-k: returns (col_idx int32 [nnz], scores fp32 [H,Vb,Kb] or
+    None, mask uint8 [H,Qb,Kb] or None)."""
+    if prep.q_hi is None:
+        raise ValueError("prepare_qkv was called without pooling")
+    dev = prep.q_perm.device
+    nnz = policy.nnz(prep.heads)
+    col_idx = torch.empty(nnz, dtype=torch.int32, device=dev)
+    scores = (torch.empty((prep.heads, policy.scored_rows, policy.k_blocks), dtype=torch.float32, device=dev)
+              if want_scores else None)
+    mask = (torch.empty((prep.heads, policy.q_blocks, policy.k_blocks), dtype=torch.uint8, device=dev)
+            if want_mask else None)
+    _lib.call("dfs_block_score_topk", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi), _ptr(prep.k_lo),
+              prep.heads, prep.head_dim, prep.layout.tile, *_policy_args(policy), _ptr(row_ptr),
+              _ptr(col_idx), _ptr(scores), _ptr(mask), _stream(prep.q_perm))
+    return col_idx, scores, mask
+
+
+def topk_from_scores(scores: torch.Tensor, policy: TopkPolicy, row_ptr: torch.Tensor,
+                     want_mask: bool = False):
+    """Top-k of given fp32 block scores [H, scored_rows, Kb] under ``policy``;
+    returns (col_idx, mask or None)."""
+    _require_device(scores, row_ptr)
+    if scores.dtype != torch.float32 or scores.dim() != 3:
+        raise ValueError("scores must be fp32 [H, rows, Kb]")
+    heads = scores.shape[0]
+    if scores.shape[1:] != (policy.scored_rows, policy.k_blocks):
+        raise ValueError(f"scores shape {tuple(scores.shape)} does not match the policy")
+    scores = scores.contiguous()
+    col_idx = torch.empty(policy.nnz(heads), dtype=torch.int32, device=scores.device)
+    mask = (torch.empty((heads, policy.q_blocks, policy.k_blocks), dtype=torch.uint8, device=scores.device)
+            if want_mask else None)
+    _lib.call("dfs_topk_from_scores", _ptr(scores), heads, *_policy_args(policy), _ptr(row_ptr),
+              _ptr(col_idx), _ptr(mask), _stream(scores))
+    return col_idx, mask
+
+
+def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale: Optional[float] = None,
+            out_dtype: Optional[torch.dtype] = None, out_perm: Optional[torch.Tensor] = None,
+            want_lse: bool = False, out: Optional[torch.Tensor] = None):
+    """Block-sparse attention over the CSR mask. Returns out [1, H, L, D] —
+    original token order when ``out_perm`` is given, execution order otherwise —
+    and the fp32 log-sum-exp [H, L] (execution order) when ``want_lse``."""
+    _require_device(row_ptr, col_idx, out_perm, out)
+    L = prep.layout.seq_len
+    out_dtype = out_dtype or prep.dtype
+    if out is None:
+        out = torch.empty((1, prep.heads, L, prep.head_dim), dtype=out_dtype, device=prep.q_perm.device)
+    elif out.dtype != out_dtype or not out.is_contiguous() or out.numel() != prep.heads * L * prep.head_dim:
+        raise ValueError("out must be a contiguous [1, H, L, D] tensor of out_dtype")
+    lse = torch.empty((prep.heads, L), dtype=torch.float32, device=out.device) if want_lse else None
+    scale = 1.0 / math.sqrt(prep.head_dim) if scale is None else float(scale)
+    _lib.call("dfs_bsa_fwd", _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(row_ptr),
+              _ptr(col_idx), prep.heads, L, prep.head_dim, DTYPE_CODE[prep.dtype],
+              DTYPE_CODE[prep.pv_dtype], scale, _ptr(out), DTYPE_CODE[out_dtype], _ptr(out_perm),
+              _ptr(lse), _stream(prep.q_perm))
+    return (out, lse) if want_lse else out
+
+
+def mask_to_csr(mask: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """bool/uint8 [H, Qb, Kb] mask -> (row_ptr int32 [H*Qb+1], col_idx int32).
+    Reads the total count back to the host once to size col_idx."""
+    _require_device(mask)
+    m = mask.contiguous()
+    if m.dtype == torch.bool:
+        m = m.view(torch.uint8)
+    rows = m.numel() // m.shape[-1]
+    counts = torch.empty(rows, dtype=torch.int32, device=m.device)
+    _lib.call("dfs_mask_row_counts", _ptr(m), rows, m.shape[-1], _ptr(counts), _stream(m))
+    row_ptr = torch.zeros(rows + 1, dtype=torch.int32, device=m.device)
+    torch.cumsum(counts, 0, out=row_ptr[1:])
+    nnz = int(row_ptr[-1].item())
+    col_idx = torch.empty(max(nnz, 1), dtype=torch.int32, device=m.device)
+    _lib.call("dfs_mask_to_csr", _ptr(m), rows, m.shape[-1], _ptr(row_ptr), _ptr(col_idx), _stream(m))
+    return row_ptr, col_idx[:nnz] if nnz else col_idx
+
+
+def csr_to_mask(row_ptr: torch.Tensor, col_idx: torch.Tensor, heads: int, q_blocks: int,
+                k_blocks: int) -> torch.Tensor:
+    """CSR -> bool mask [H, Qb, Kb] on the device."""
+    _require_device(row_ptr, col_idx)
+    mask = torch.empty((heads, q_blocks, k_blocks), dtype=torch.uint8, device=row_ptr.device)
+    _lib.call("dfs_csr_to_mask", _ptr(row_ptr), _ptr(col_idx), heads * q_blocks, k_blocks, _ptr(mask),
+              _stream(row_ptr))
+    return mask.view(torch.bool)
+
+
+def hilbert3d_perm(f: int, h: int, w: int) -> torch.Tensor:
+    """3D Hilbert order of an f x h x w grid (host function of the library)."""
+    out = torch.empty(f * h * w, dtype=torch.int64)
+    _lib.call("dfs_hilbert3d_perm", f, h, w, _ptr(out))
+    return out

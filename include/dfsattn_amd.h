@@ -1,0 +1,185 @@
+/*
+ * dfsattn_amd.h — C-ABI of the MI355X (gfx950) DFS sparse-attention hot path.
+ *
+ * Every entry point returns 0 on success and a non-zero status on failure;
+ * dfs_last_error() then returns a thread-local message. Pointers are raw
+ * device pointers unless stated otherwise, sizes are int64, and every GPU
+ * entry point enqueues work on the caller's stream and never synchronises.
+ * None of them allocates device memory: callers own every buffer.
+ *
+ * Tensor layouts (B = 1 everywhere, as in the reference, which asserts it at
+ * dfsattn/attention_wan.py:222,288):
+ *   - q, k, v, out        [H][L][D] row-major (the reference's [1,H,L,D]).
+ *   - perm                int32 [L]; execution (Hilbert) row i reads source
+ *                         row perm[i]. For HunyuanVideo the tail L_video..L-1
+ *                         is the identity (dfsattn/attention_hyvideo.py:161-174).
+ *   - q_perm, k_perm      [H][R][D], R = ceil(L/128)*128 (rows >= L are zero).
+ *   - v_t                 [H][R/128][D][128] in the PV operand dtype (bf16 or
+ *                         f16): each 128-token block transposed, tokens in
+ *                         a fixed order inside every 16-token group.
+ *   - pooled hi / lo      bf16 [H][tiles][D]: tile mean split as hi + lo.
+ *   - row_ptr, col_idx    int32 CSR over the [H][Qb][Kb] block mask;
+ *                         row r = h*Qb + qb, columns ascending.
+ *
+ * dtype codes: 0 = bf16, 1 = f16, 2 = f32.
+ */
+#ifndef DFSATTN_AMD_H
+#define DFSATTN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* dfs_stream_t; /* == hipStream_t */
+
+enum { DFS_DTYPE_BF16 = 0, DFS_DTYPE_F16 = 1, DFS_DTYPE_F32 = 2 };
+
+/* Last error message of the calling thread ("" if none). */
+const char* dfs_last_error(void);
+
+/* ABI version; bumped whenever a signature below changes. */
+int dfs_abi_version(void);
+
+/*
+ * Host function. Writes the 3D Hilbert order of an f x h x w latent grid:
+ * perm_out[i] = z*h*w + y*w + x of the i-th token along the curve, with the
+ * coordinate columns (x, y, z) = (w-index, h-index, f-index) and
+ * num_bits = max(1, ceil(log2(max(f, h, w)))).
+ * Replaces dfsattn/utils/order.py:206-258 (hilbert3d_perm), including the
+ * numpy-hilbert-curve encode() it calls at order.py:250.
+ */
+int dfs_hilbert3d_perm(int64_t f, int64_t h, int64_t w, int64_t* perm_out);
+
+/*
+ * Bit-exact row gather: dst[h][i] = src[h][perm[i]] for i < n_perm and zero
+ * rows for n_perm <= i < dst_rows. row_bytes must be a multiple of 2.
+ * Out-of-range perm entries produce zero rows.
+ * Replaces DFS_Attention._apply_permutation_in_place, tensor[:, :, perm, :]
+ * (dfsattn/attention_wan.py:128-135; attention_hyvideo.py:177-184).
+ */
+int dfs_permute_gather(const void* src, const int32_t* perm, void* dst,
+                       int64_t heads, int64_t src_rows, int64_t n_perm,
+                       int64_t dst_rows, int64_t row_bytes, dfs_stream_t stream);
+
+/*
+ * Bit-exact row scatter (inverse permutation): dst[h][perm[i]] = src[h][i]
+ * for i < n_perm. Rows of dst not named by perm are left untouched.
+ * Replaces DFS_Attention._apply_inverse_permutation, tensor[:, :, inv, :]
+ * with inv[perm] = arange (dfsattn/attention_wan.py:113-125, 138-145).
+ */
+int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst,
+                        int64_t heads, int64_t src_rows, int64_t n_perm,
+                        int64_t dst_rows, int64_t row_bytes, dfs_stream_t stream);
+
+/*
+ * Fused permute of Q, K, V into the attention operand layouts plus mean
+ * pooling of Q and K over tile_size-token tiles in the scoring layout.
+ *   dtype        0 (bf16) or 1 (f16) for q, k, v, q_perm, k_perm.
+ *   video_len    L for Wan; the video token count for HunyuanVideo. The
+ *                scoring layout is [video | zero pad to 128 | text | zero
+ *                pad to ceil(L/128)*128] (attention_hyvideo.py:331-365;
+ *                for Wan, attention_wan.py:176-189).
+ *   pv_dtype     0: v_t holds the bf16 bits of v; 1: v_t holds v in f16.
+ *   q_pool_*     [H][ceil(video_len/128)*128/tile][D] (may all be NULL to skip
+ *   k_pool_*     [H][ceil(L/128)*128/tile][D]          pooling: cached steps).
+ *   v_overflow   optional int32 flag, set to 1 when pv_dtype = 1 and some
+ *                |v| exceeds the f16 range.
+ * Replaces the q/k/v gathers of attention_wan.py:173-174, 338-340 and the
+ * padding + tile means of attention_wan.py:176-205.
+ */
+int dfs_prepare_qkv(const void* q, const void* k, const void* v,
+                    const int32_t* perm, int64_t heads, int64_t seq_len,
+                    int64_t head_dim, int dtype, int64_t video_len,
+                    int64_t tile_size, int pv_dtype,
+                    void* q_perm, void* k_perm, void* v_t,
+                    uint16_t* q_pool_hi, uint16_t* q_pool_lo,
+                    uint16_t* k_pool_hi, uint16_t* k_pool_lo,
+                    int32_t* v_overflow, dfs_stream_t stream);
+
+/*
+ * Hierarchical block scoring and top-k in one kernel: pooled QK^T * D^-1/2
+ * (bf16 MFMA on the hi/lo split), softmax over all key tiles, sums of tile
+ * probabilities per 128x128 block, then per-row top-k.
+ * Row selection policy (same as dfs_topk_from_scores):
+ *   scored_rows  number of query-block rows that carry scores
+ *                (ceil(video_len/128)).
+ *   n_cand       candidate columns 0..n_cand-1 compete for k_pick slots.
+ *   dense_col    columns dense_col..Kb-1 are always kept in scored rows.
+ *   dense_row    rows dense_row..Qb-1 keep every column.
+ *   row_ptr      CSR row offsets [H*Qb+1] consistent with the policy.
+ *   col_idx      CSR columns (ascending per row).
+ *   scores_out   optional fp32 [H][scored_rows][Kb] block scores.
+ *   mask_out     optional uint8 [H][Qb][Kb] block mask.
+ * Ties are broken by (score descending, column ascending).
+ * Replaces _compute_tile_score + _compute_block_mask
+ * (attention_wan.py:157-261; attention_hyvideo.py:310-501).
+ */
+int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
+                         const uint16_t* k_pool_hi, const uint16_t* k_pool_lo,
+                         int64_t heads, int64_t head_dim, int64_t tile_size,
+                         int64_t q_blocks, int64_t k_blocks,
+                         int64_t scored_rows, int64_t n_cand, int64_t k_pick,
+                         int64_t dense_col, int64_t dense_row,
+                         const int32_t* row_ptr, int32_t* col_idx,
+                         float* scores_out, uint8_t* mask_out,
+                         dfs_stream_t stream);
+
+/*
+ * Top-k from given fp32 block scores [H][scored_rows][Kb] with the policy
+ * above; emits CSR columns and an optional uint8 mask. Given the same fp32
+ * scores it selects exactly the set torch.topk + scatter_ selects when no tie
+ * straddles the k-th place (attention_wan.py:248-253;
+ * attention_hyvideo.py:431-443, 491-501).
+ */
+int dfs_topk_from_scores(const float* scores, int64_t heads,
+                         int64_t q_blocks, int64_t k_blocks,
+                         int64_t scored_rows, int64_t n_cand, int64_t k_pick,
+                         int64_t dense_col, int64_t dense_row,
+                         const int32_t* row_ptr, int32_t* col_idx,
+                         uint8_t* mask_out, dfs_stream_t stream);
+
+/*
+ * Block-sparse flash-attention forward over the kept 128x128 blocks.
+ *   q_perm, k_perm, v_t  as produced by dfs_prepare_qkv (dtype, pv_dtype).
+ *   scale                softmax scale (the reference passes None -> D^-1/2).
+ *   out                  out_dtype 0/1/2; when out_perm is NULL, out is
+ *                        [H][L][D] in execution order; otherwise row i is
+ *                        written to out[h][out_perm[i]] (fused unpermute).
+ *   lse                  optional fp32 [H][L] natural-log sum-exp (execution
+ *                        order).
+ * Keys >= L in the last block are masked out; rows with no kept block give 0.
+ * Replaces block_sparse_attn_func (attention_wan.py:379-386;
+ * attention_hyvideo.py:1075-1082) and, with out_perm, the final inverse
+ * gather (attention_wan.py:390).
+ */
+int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v_t,
+                const int32_t* row_ptr, const int32_t* col_idx,
+                int64_t heads, int64_t seq_len, int64_t head_dim, int dtype,
+                int pv_dtype, float scale, void* out, int out_dtype,
+                const int32_t* out_perm, float* lse, dfs_stream_t stream);
+
+/* uint8/bool block mask [H][Qb][Kb] -> per-row counts int32 [H*Qb].
+ * Part of the bool-mask interface of block_sparse_attn_func
+ * (base_blockmask, attention_wan.py:359). */
+int dfs_mask_row_counts(const uint8_t* mask, int64_t rows, int64_t k_blocks,
+                        int32_t* counts, dfs_stream_t stream);
+
+/* uint8/bool block mask -> CSR columns given row_ptr (exclusive scan of the
+ * counts above). */
+int dfs_mask_to_csr(const uint8_t* mask, int64_t rows, int64_t k_blocks,
+                    const int32_t* row_ptr, int32_t* col_idx,
+                    dfs_stream_t stream);
+
+/* CSR -> uint8 block mask [rows][Kb] (the reference's cached bool
+ * block_mask, attention_wan.py:252-253, 465-470). */
+int dfs_csr_to_mask(const int32_t* row_ptr, const int32_t* col_idx,
+                    int64_t rows, int64_t k_blocks, uint8_t* mask,
+                    dfs_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFSATTN_AMD_H */

@@ -1,0 +1,327 @@
+"""CPU restatement of DFSAttn's sparse-attention hot path.
+
+TEST INFRASTRUCTURE ONLY. Nothing in the product imports this module: only
+``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may use it, and only as the checker (or the timed CPU baseline),
+never as a fallback for the HIP path.
+
+Each function restates the reference (``codesiena/DFSattn``) at the cited
+``file:line`` in plain numpy / fp32 torch on the CPU. How each is pinned
+(see ``tests/test_oracle.py``):
+
+* ``hilbert_encode`` / ``hilbert3d_perm`` (dfsattn/utils/order.py:206-258,
+  numpy-hilbert-curve>=1.0.0 ``encode``, requirements.txt:19): pinned by
+  closed forms (1 bit per axis = inverse Gray code of the interleaved
+  coordinate bits, axis 0 most significant), the Hilbert-curve invariants
+  (bijection, unit steps on full 2^b cubes, index 0 at the origin) and an
+  independent C implementation. The exact numpy-hilbert-curve bit convention
+  beyond these is **parity unpinned** (the package is absent offline and the
+  reference ships no fixture for it).
+* ``compute_cache_schedule`` (dfsattn/attention_wan.py:41-66): pinned by the
+  reference's own known-answer test (tests/test_flashinfer64_attention.py:122-157).
+* ``tile_scores`` / ``block_scores`` (attention_wan.py:157-246,
+  attention_hyvideo.py:310-422): pinned by a brute-force loop restatement on
+  tiny inputs and the invariant that every scored row of block scores sums to
+  block/tile (softmax rows sum to one).
+* ``mask_from_scores_*`` (attention_wan.py:248-253, attention_hyvideo.py:424-501):
+  pinned against ``torch.topk`` + ``scatter_`` (the reference's own calls) on
+  tie-free scores, and by policy invariants (row counts, dense text columns/rows).
+* ``masked_attention`` (block_sparse_attn_func semantics,
+  attention_wan.py:379-386): pinned against dense ``torch.softmax`` attention
+  with an explicit token mask, and equals dense attention for an all-True mask.
+  The external kernel's own rounding is parity unpinned (no fixture exists);
+  the contract is the fp32 masked-dense closed form.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import numpy as np
+import torch
+
+BLOCK = 128
+
+
+# --------------------------------------------------------------------------
+# a1: Hilbert order (dfsattn/utils/order.py:206-258)
+# --------------------------------------------------------------------------
+
+def hilbert_encode(locs: np.ndarray, num_dims: int, num_bits: int) -> np.ndarray:
+    """Hilbert integers of integer points ``locs[..., num_dims]``.
+
+    Restates numpy-hilbert-curve's ``encode`` (called at order.py:250) in its
+    bit-array form: big-endian coordinate bits; for each bit level (most
+    significant first) and each axis, invert the lower bits of axis 0 where the
+    axis bit is set, else exchange the lower bits of axis 0 and the axis
+    (Skilling 2004); interleave level by level with axis 0 first; Gray-decode.
+    """
+    locs = np.asarray(locs, dtype=np.int64)
+    if locs.shape[-1] != num_dims:
+        raise ValueError("last dimension of locs must equal num_dims")
+    if num_dims * num_bits > 63:
+        raise ValueError("num_dims * num_bits must not exceed 63")
+    flat = locs.reshape(-1, num_dims)
+    shifts = np.arange(num_bits - 1, -1, -1, dtype=np.int64)
+    # gray[n, dim, bit] with bit 0 the most significant.
+    gray = ((flat[:, :, None] >> shifts[None, None, :]) & 1).astype(bool)
+    for bit in range(num_bits):
+        for dim in range(num_dims):
+            mask = gray[:, dim, bit][:, None]
+            gray[:, 0, bit + 1:] ^= mask
+            to_flip = (~mask) & (gray[:, 0, bit + 1:] ^ gray[:, dim, bit + 1:])
+            gray[:, dim, bit + 1:] ^= to_flip
+            gray[:, 0, bit + 1:] ^= to_flip
+    inter = np.swapaxes(gray, 1, 2).reshape(-1, num_bits * num_dims)
+    binary = np.logical_xor.accumulate(inter, axis=1)
+    weights = (np.uint64(1) << np.arange(inter.shape[1] - 1, -1, -1, dtype=np.uint64))
+    codes = (binary.astype(np.uint64) * weights[None, :]).sum(axis=1, dtype=np.uint64)
+    return codes.reshape(locs.shape[:-1])
+
+
+def hilbert3d_perm(f: int, h: int, w: int) -> np.ndarray:
+    """order.py:206-258: linear indices z*h*w + y*w + x in Hilbert order, with
+    coordinate columns [x, y, z] and num_bits = max(1, ceil(log2(max dim)))."""
+    max_dim = max(w, h, f)
+    num_bits = max(1, math.ceil(math.log2(max_dim))) if max_dim > 1 else 1
+    z, y, x = np.meshgrid(np.arange(f), np.arange(h), np.arange(w), indexing="ij")
+    linear = (z * (h * w) + y * w + x).reshape(-1)
+    coords = np.stack([x.reshape(-1), y.reshape(-1), z.reshape(-1)], axis=1)
+    codes = hilbert_encode(coords, 3, num_bits)
+    order = np.argsort(codes, kind="stable")
+    return linear[order].astype(np.int64)
+
+
+# --------------------------------------------------------------------------
+# a4: refresh schedule (attention_wan.py:41-66 == attention_hyvideo.py:40-65)
+# --------------------------------------------------------------------------
+
+def compute_cache_schedule(step_idx: int, skip_steps: int, cache_interval: int,
+                           sparsity: float, sparsity_dcrt: float) -> Tuple[bool, float]:
+    if cache_interval <= 0:
+        raise ValueError("cache_interval must be greater than 0.")
+    if step_idx < skip_steps:
+        return False, sparsity
+    raw = (step_idx - skip_steps) // cache_interval
+    max_valid = max(0, math.ceil(sparsity / sparsity_dcrt) - 1) if sparsity_dcrt > 0 else raw
+    idx = min(raw, max_valid)
+    refresh = raw <= max_valid and (step_idx - skip_steps) % cache_interval == 0
+    cur = min(1.0, max(0.0, sparsity - idx * sparsity_dcrt))
+    return refresh, cur
+
+
+def topk_count(sparse_ratio: float, k_blocks: int) -> int:
+    """attention_wan.py:248 / attention_hyvideo.py:432."""
+    return max(1, int(sparse_ratio * k_blocks))
+
+
+# --------------------------------------------------------------------------
+# a2/a3: permutation (attention_wan.py:113-145, attention_hyvideo.py:154-194)
+# --------------------------------------------------------------------------
+
+def full_permutation(video_perm: torch.Tensor, seq_len: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """perm = cat(video_perm, arange(video_len, seq_len)); inv[perm] = arange."""
+    video_perm = torch.as_tensor(video_perm, dtype=torch.long)
+    vlen = video_perm.numel()
+    perm = torch.cat([video_perm, torch.arange(vlen, seq_len, dtype=torch.long)]) if seq_len > vlen else video_perm
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel(), dtype=torch.long)
+    return perm, inv
+
+
+def apply_permutation(x: torch.Tensor, perm: torch.Tensor) -> torch.Tensor:
+    """tensor[:, :, perm, :] (attention_wan.py:134)."""
+    return x[:, :, perm, :].contiguous()
+
+
+# --------------------------------------------------------------------------
+# a5/a6: tile scores, block scores and the top-k mask
+# --------------------------------------------------------------------------
+
+def _scoring_layout(x_perm: torch.Tensor, seq_len: int, video_len: int, block: int) -> torch.Tensor:
+    """[video | zeros to a block multiple | text | zeros to ceil(L/block)*block]
+    (attention_wan.py:176-189; attention_hyvideo.py:331-365)."""
+    bsz, heads, _, dim = x_perm.shape
+    vb = math.ceil(video_len / block)
+    kb = math.ceil(seq_len / block)
+    parts = [x_perm[:, :, :video_len]]
+    pad = vb * block - video_len
+    if pad:
+        parts.append(x_perm.new_zeros(bsz, heads, pad, dim))
+    if seq_len > video_len:
+        parts.append(x_perm[:, :, video_len:])
+    out = torch.cat(parts, dim=2)
+    if out.shape[2] > kb * block:
+        raise RuntimeError("scoring layout exceeds ceil(L/block) blocks; the reference's .view fails")
+    if out.shape[2] < kb * block:
+        out = torch.cat([out, x_perm.new_zeros(bsz, heads, kb * block - out.shape[2], dim)], dim=2)
+    return out
+
+
+def pooled_tiles(q_perm: torch.Tensor, k_perm: torch.Tensor, tile: int, block: int = BLOCK,
+                 video_len: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Tile means of the scoring layout: queries over the video part, keys over
+    everything (attention_wan.py:192-205; attention_hyvideo.py:367-381)."""
+    seq_len = q_perm.shape[2]
+    video_len = seq_len if video_len is None else video_len
+    qs = _scoring_layout(q_perm.float(), seq_len, video_len, block)
+    ks = _scoring_layout(k_perm.float(), seq_len, video_len, block)
+    bsz, heads, _, dim = qs.shape
+    vpad_len = math.ceil(video_len / block) * block
+    qt = qs[:, :, :vpad_len].reshape(bsz, heads, vpad_len // tile, tile, dim).mean(dim=3)
+    kt = ks.reshape(bsz, heads, ks.shape[2] // tile, tile, dim).mean(dim=3)
+    return qt, kt
+
+
+def tile_scores(q_perm: torch.Tensor, k_perm: torch.Tensor, tile: int, block: int = BLOCK,
+                video_len: Optional[int] = None) -> torch.Tensor:
+    """fp32 softmax(Qt Kt^T / sqrt(D)) over all key tiles, [B, H, Qt, Kt]
+    (attention_wan.py:207; attention_hyvideo.py:383)."""
+    qt, kt = pooled_tiles(q_perm, k_perm, tile, block, video_len)
+    scale = 1.0 / math.sqrt(q_perm.shape[-1])
+    return (qt @ kt.transpose(-2, -1) * scale).softmax(dim=-1)
+
+
+def block_scores(q_perm: torch.Tensor, k_perm: torch.Tensor, tile: int, block: int = BLOCK,
+                 video_len: Optional[int] = None, head_chunk: int = 4) -> torch.Tensor:
+    """Block sums of tile probabilities, fp32 [H, Vb, Kb]
+    (attention_wan.py:243-246; attention_hyvideo.py:419-422), computed a few
+    heads at a time to bound memory at the full configurations."""
+    heads = q_perm.shape[1]
+    tpb = block // tile
+    outs = []
+    for h0 in range(0, heads, head_chunk):
+        ts = tile_scores(q_perm[:, h0:h0 + head_chunk], k_perm[:, h0:h0 + head_chunk], tile, block, video_len)
+        b, hh, qt, kt = ts.shape
+        outs.append(ts.view(b, hh, qt // tpb, tpb, kt // tpb, tpb).sum(dim=(3, 5))[0])
+    return torch.cat(outs, dim=0)
+
+
+def select_topk(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """Bool mask of the k largest entries per row under the total order
+    (score descending, column ascending)."""
+    s = scores.detach().cpu().double().numpy()
+    rows = s.reshape(-1, s.shape[-1])
+    order = np.lexsort((np.broadcast_to(np.arange(rows.shape[1]), rows.shape), -rows), axis=1)
+    mask = np.zeros(rows.shape, dtype=bool)
+    np.put_along_axis(mask, order[:, :k], True, axis=1)
+    return torch.from_numpy(mask.reshape(s.shape))
+
+
+def boundary_ties(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """Rows whose k-th and (k+1)-th largest scores are equal (where torch.topk's
+    choice is implementation-defined)."""
+    if k >= scores.shape[-1]:
+        return torch.zeros(scores.shape[:-1], dtype=torch.bool)
+    srt = torch.sort(scores.double(), dim=-1, descending=True).values
+    return srt[..., k - 1] == srt[..., k]
+
+
+def mask_from_scores_wan(scores: torch.Tensor, sparse_ratio: float) -> torch.Tensor:
+    """attention_wan.py:248-253: k = max(1, int(s * Kb)); top-k per row."""
+    return select_topk(scores, topk_count(sparse_ratio, scores.shape[-1]))
+
+
+def mask_from_scores_hunyuan(scores: torch.Tensor, sparse_ratio: float, seq_len: int,
+                             video_len: int, block: int = BLOCK) -> torch.Tensor:
+    """attention_hyvideo.py:424-501 (top-k branch): the video budget
+    k - text_blocks is chosen among the first video_len // block columns, the
+    remaining columns are kept, and rows >= video_len // block are dense when
+    text tokens exist."""
+    heads, vb, kb = scores.shape
+    qb = kb
+    dense_start = video_len // block
+    text_blocks = max(0, kb - dense_start)
+    topk = topk_count(sparse_ratio, kb)
+    video_mask = torch.zeros(heads, vb, kb, dtype=torch.bool)
+    if text_blocks > 0:
+        budget = topk - text_blocks
+        if budget <= 0:
+            raise AssertionError("num_video_blocks_to_select must be non-negative")
+        if budget > dense_start:
+            raise RuntimeError("selected index k out of range")
+        video_mask[..., :dense_start] = select_topk(scores[..., :dense_start], budget)
+        video_mask[..., dense_start:] = True
+    else:
+        video_mask = select_topk(scores, topk)
+    mask = torch.zeros(heads, qb, kb, dtype=torch.bool)
+    mask[:, :vb] = video_mask
+    if seq_len > video_len:
+        mask[:, dense_start:] = True
+    return mask
+
+
+def mask_from_scores_torch(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """The reference's literal calls: torch.topk + scatter_ (attention_wan.py:249-253)."""
+    _, idx = torch.topk(scores, k=k, dim=-1)
+    return torch.zeros_like(scores, dtype=torch.bool).scatter_(-1, idx, True)
+
+
+# --------------------------------------------------------------------------
+# a8: block-masked attention (block_sparse_attn_func semantics)
+# --------------------------------------------------------------------------
+
+def masked_attention(q_perm: torch.Tensor, k_perm: torch.Tensor, v_perm: torch.Tensor,
+                     mask: torch.Tensor, block: int = BLOCK, scale: Optional[float] = None,
+                     heads: Optional[list] = None, q_blocks: Optional[list] = None) -> torch.Tensor:
+    """fp32 softmax(Q K^T * scale) V where query block i sees the key blocks
+    kept in mask[h, i] (tokens past L excluded). Returns [B, H, L, D] fp32 with
+    rows outside the requested heads / query blocks left at zero.
+    Rows with no kept block are zero."""
+    q = q_perm.float()
+    k = k_perm.float()
+    v = v_perm.float()
+    _, n_heads, seq_len, dim = q.shape
+    scale = 1.0 / math.sqrt(dim) if scale is None else scale
+    out = torch.zeros_like(q)
+    n_blocks = math.ceil(seq_len / block)
+    heads = range(n_heads) if heads is None else heads
+    for h in heads:
+        for i in (range(n_blocks) if q_blocks is None else q_blocks):
+            cols = torch.nonzero(mask[h, i]).flatten().tolist()
+            if not cols:
+                continue
+            tok = torch.cat([torch.arange(c * block, min((c + 1) * block, seq_len)) for c in cols])
+            qi = q[0, h, i * block:(i + 1) * block]
+            s = (qi @ k[0, h, tok].T) * scale
+            p = torch.softmax(s, dim=-1)
+            out[0, h, i * block:(i + 1) * block] = p @ v[0, h, tok]
+    return out
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    token_mask: Optional[torch.Tensor] = None, scale: Optional[float] = None) -> torch.Tensor:
+    """fp32 attention with an optional [H, L, L] bool token mask (closed form)."""
+    q, k, v = q.float(), k.float(), v.float()
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    s = (q @ k.transpose(-2, -1)) * scale
+    if token_mask is not None:
+        s = s.masked_fill(~token_mask, float("-inf"))
+    return torch.softmax(s, dim=-1) @ v
+
+
+def expand_block_mask(mask: torch.Tensor, seq_len: int, block: int = BLOCK) -> torch.Tensor:
+    """[H, Qb, Kb] block mask -> [H, L, L] token mask."""
+    tok = mask.repeat_interleave(block, dim=1).repeat_interleave(block, dim=2)
+    return tok[:, :seq_len, :seq_len]
+
+
+# --------------------------------------------------------------------------
+# Whole call (attention_wan.py:394-547 native path; attention_hyvideo.py:1090-1286)
+# --------------------------------------------------------------------------
+
+def dfs_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, video_perm: torch.Tensor,
+                            sparse_ratio: float, tile: int, block: int = BLOCK,
+                            video_len: Optional[int] = None):
+    """Permute, score, select, attend, unpermute. Returns (out fp32 [1,H,L,D]
+    in the original order, bool mask [H,Qb,Kb], fp32 block scores)."""
+    seq_len = q.shape[2]
+    perm, inv = full_permutation(video_perm, seq_len)
+    qp, kp, vp = apply_permutation(q, perm), apply_permutation(k, perm), apply_permutation(v, perm)
+    scores = block_scores(qp, kp, tile, block, video_len)
+    if video_len is None:
+        mask = mask_from_scores_wan(scores, sparse_ratio)
+    else:
+        mask = mask_from_scores_hunyuan(scores, sparse_ratio, seq_len, video_len, block)
+    out = masked_attention(qp, kp, vp, mask, block)
+    return out[:, :, inv, :], mask, scores

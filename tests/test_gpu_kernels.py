@@ -1,0 +1,231 @@
+"""Kernel-level parity of the HIP path against the CPU oracle (GPU only).
+
+Bit-exact: permute gather/scatter, operand preparation, top-k from identical
+fp32 scores. Tolerance: pooled tiles (hi+lo split, rel 2e-5), block scores
+(rel 2e-3 against fp32), attention output in fp32 (max-abs 2e-2, mean-rel 1e-3
+against fp32 masked-dense attention; mean-rel = mean|out - ref| / mean|ref|).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from dfsattn_amd import ops
+from dfsattn_amd.layout import ScoringLayout, hunyuan_policy, wan_policy, dense_policy
+from oracle import dfs_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _swap23(s):
+    return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1)
+
+
+def vt_reference(v_perm_padded: torch.Tensor, dtype) -> torch.Tensor:
+    """[H, R, D] (execution order, zero rows past L) -> [H, R/128, D, 128]
+    with tokens of each 16-group in swap23 order."""
+    h, r, d = v_perm_padded.shape
+    idx = torch.tensor([_swap23(s) for s in range(16)])
+    x = v_perm_padded.view(h, r // 128, 8, 16, d)[:, :, :, idx, :]
+    return x.reshape(h, r // 128, 128, d).transpose(2, 3).to(dtype).contiguous()
+
+
+def mean_rel(out, ref):
+    return float((out.double() - ref.double()).abs().mean() / ref.double().abs().mean())
+
+
+@pytest.mark.parametrize("dtype,d,length,n", [
+    (torch.bfloat16, 128, 67, 61),   # the reference's own Triton-permute test shape
+    (torch.float32, 64, 1000, 1000),
+    (torch.float16, 3, 257, 200),    # 6-byte rows: 2-byte vector path
+])
+def test_permute_gather_scatter_bit_exact(dev, dtype, d, length, n):
+    torch.manual_seed(40)
+    src = torch.randn((1, 3, length, d), dtype=dtype)
+    perm = torch.randperm(n)
+    perm_d = perm.to(dev, torch.int32)
+    out = ops.permute_gather(src.to(dev), perm_d, rows=n + 5).cpu()
+    assert torch.equal(out[:, :, :n], src[:, :, perm])
+    assert torch.count_nonzero(out[:, :, n:]) == 0
+    # inverse permutation: scatter of the gathered rows restores the source rows
+    back = torch.zeros_like(src).to(dev)
+    ops.permute_scatter(out[:, :, :n].contiguous().to(dev), perm_d, out=back)
+    back = back.cpu()
+    assert torch.equal(back[:, :, perm], src[:, :, perm])
+    untouched = torch.ones(length, dtype=torch.bool)
+    untouched[perm] = False
+    assert torch.count_nonzero(back[:, :, untouched]) == 0
+
+
+@pytest.mark.parametrize("case", ["wan_tail", "wan_even", "hunyuan_text", "hunyuan_no_text", "d64_tile32"])
+def test_prepare_qkv_matches_oracle(dev, case):
+    heads, d, tile, dtype, pv = 2, 128, 16, torch.bfloat16, torch.float16
+    if case == "wan_tail":
+        length, video = 1000, 1000
+    elif case == "wan_even":
+        length, video = 1024, 1024
+    elif case == "hunyuan_text":
+        length, video = 1000 + 60, 1000
+    elif case == "hunyuan_no_text":
+        length, video = 1000, 1000
+    else:
+        length, video, d, tile, pv = 777, 777, 64, 32, torch.bfloat16
+    torch.manual_seed(7)
+    q, k, v = (torch.randn((1, heads, length, d)).to(dtype) for _ in range(3))
+    vperm = torch.randperm(video)
+    perm, _ = orc.full_permutation(vperm, length)
+    layout = ScoringLayout(length, video, tile)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout, pv_dtype=pv,
+                           check_overflow=True)
+    qp, kp, vp = (orc.apply_permutation(x, perm) for x in (q, k, v))
+    R = layout.rows
+    pad = lambda x: torch.cat([x[0], x.new_zeros(heads, R - length, d)], dim=1)
+    assert torch.equal(prep.q_perm.cpu(), pad(qp))
+    assert torch.equal(prep.k_perm.cpu(), pad(kp))
+    assert torch.equal(prep.v_t.cpu(), vt_reference(pad(vp), pv))
+    assert int(prep.v_overflow.item()) == 0
+    qt, kt = orc.pooled_tiles(qp, kp, tile, 128, video)
+    for hi, lo, ref in ((prep.q_hi, prep.q_lo, qt[0]), (prep.k_hi, prep.k_lo, kt[0])):
+        got = hi.cpu().float() + lo.cpu().float()
+        assert got.shape == ref.shape
+        assert torch.allclose(got, ref, rtol=2e-5, atol=1e-6), float((got - ref).abs().max())
+
+
+def _random_scores(heads, rows, cols, seed, ties=False):
+    g = torch.Generator().manual_seed(seed)
+    s = torch.rand((heads, rows, cols), generator=g)
+    if ties:
+        s = torch.round(s * 8) / 8  # many exact ties, some straddling the k-th place
+    return s
+
+
+@pytest.mark.parametrize("cols,ratio,ties", [(591, 0.3, False), (8, 0.3, False), (100, 0.05, True),
+                                             (931, 0.3, True), (2048, 0.5, False)])
+def test_topk_from_scores_wan_bit_exact(dev, cols, ratio, ties):
+    layout = ScoringLayout(cols * 128 - 7, cols * 128 - 7, 16)
+    pol = wan_policy(layout, ratio)
+    heads = 3
+    scores = _random_scores(heads, pol.scored_rows, pol.k_blocks, cols, ties)
+    row_ptr = torch.from_numpy(pol.row_ptr(heads)).to(dev)
+    col_idx, mask = ops.topk_from_scores(scores.to(dev), pol, row_ptr, want_mask=True)
+    want = orc.mask_from_scores_wan(scores, ratio)
+    assert torch.equal(mask.cpu().bool(), want)
+    # CSR lists ascending columns of the same set
+    got = ops.csr_to_mask(row_ptr, col_idx, heads, pol.q_blocks, pol.k_blocks).cpu()
+    assert torch.equal(got, want)
+    cols_np = col_idx.cpu().numpy().reshape(heads * pol.q_blocks, pol.k_pick)
+    assert (np.diff(cols_np, axis=1) > 0).all()
+    if not ties:
+        # the reference's literal torch.topk + scatter_ selects the same set
+        assert torch.equal(want, orc.mask_from_scores_torch(scores, pol.k_pick))
+
+
+@pytest.mark.parametrize("video,text,ratio", [(118800, 256, 0.3), (1000, 60, 0.5),
+                                              (1000, 0, 0.3), (1024, 0, 0.3), (3000, 256, 0.2)])
+def test_topk_from_scores_hunyuan_policy(dev, video, text, ratio):
+    layout = ScoringLayout(video + text, video, 16)
+    pol = hunyuan_policy(layout, ratio)
+    heads = 2
+    scores = _random_scores(heads, pol.scored_rows, pol.k_blocks, video)
+    row_ptr = torch.from_numpy(pol.row_ptr(heads)).to(dev)
+    col_idx, mask = ops.topk_from_scores(scores.to(dev), pol, row_ptr, want_mask=True)
+    want = orc.mask_from_scores_hunyuan(scores, ratio, video + text, video)
+    assert torch.equal(mask.cpu().bool(), want)
+    assert torch.equal(ops.csr_to_mask(row_ptr, col_idx, heads, pol.q_blocks, pol.k_blocks).cpu(), want)
+
+
+@pytest.mark.parametrize("d,tile,video,text", [(128, 16, 4 * 16 * 16, 0), (128, 16, 3 * 20 * 21, 0),
+                                               (64, 16, 4 * 16 * 16, 0), (128, 32, 2000, 0),
+                                               (128, 16, 2000, 100), (64, 32, 1500, 100)])
+def test_block_score_topk_matches_oracle(dev, d, tile, video, text):
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+    heads = 2
+    cfg = DfsConfig("t", (1, 1, video), heads, d, torch.bfloat16, text_len=text, tile=tile, seed=3)
+    q, k, v = synth_qkv(cfg)
+    length = video + text
+    perm, _ = orc.full_permutation(torch.randperm(video, generator=torch.Generator().manual_seed(5)), length)
+    layout = ScoringLayout(length, video, tile)
+    pol = wan_policy(layout, 0.3) if text == 0 else hunyuan_policy(layout, 0.3)
+    row_ptr = torch.from_numpy(pol.row_ptr(heads)).to(dev)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout)
+    col_idx, scores, mask = ops.block_score_topk(prep, pol, row_ptr, want_scores=True, want_mask=True)
+    qp, kp = orc.apply_permutation(q, perm), orc.apply_permutation(k, perm)
+    ref = orc.block_scores(qp, kp, tile, 128, video if text else None)
+    got = scores.cpu()
+    assert got.shape == ref.shape
+    assert torch.allclose(got, ref, rtol=2e-3, atol=2e-5), float((got - ref).abs().max())
+    # every scored row of the block scores sums to block/tile
+    assert torch.allclose(got.sum(-1), torch.full_like(got.sum(-1), 128 / tile), rtol=1e-4)
+    # the fused top-k equals the oracle's selection on the same fp32 scores
+    sel = orc.mask_from_scores_wan(got, 0.3) if text == 0 else \
+        orc.mask_from_scores_hunyuan(got, 0.3, length, video)
+    assert torch.equal(mask.cpu().bool(), sel)
+    assert torch.equal(ops.csr_to_mask(row_ptr, col_idx, heads, pol.q_blocks, pol.k_blocks).cpu(), sel)
+    # and agrees with the oracle's own fp32 mask up to near-ties
+    ref_sel = orc.mask_from_scores_wan(ref, 0.3) if text == 0 else \
+        orc.mask_from_scores_hunyuan(ref, 0.3, length, video)
+    agree = (sel == ref_sel).float().mean().item()
+    assert agree > 0.995, agree
+
+
+def _run_bsa(dev, q, k, v, mask_bool, pv, out_dtype, perm=None):
+    heads, length, d = q.shape[1], q.shape[2], q.shape[3]
+    layout = ScoringLayout(length, length, 16)
+    ident = torch.arange(length, dtype=torch.int32)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident.to(dev), layout, pv_dtype=pv, pool=False)
+    row_ptr, col_idx = ops.mask_to_csr(mask_bool.to(dev))
+    out = ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=out_dtype,
+                      out_perm=None if perm is None else perm.to(dev, torch.int32))
+    return out.cpu()
+
+
+@pytest.mark.parametrize("d,length,density,pv", [
+    (128, 1000, 0.3, torch.float16), (128, 1024, 0.5, torch.float16), (64, 1000, 0.3, torch.float16),
+    (128, 3000, 0.3, torch.float16), (128, 1000, 1.0, torch.float16), (128, 1000, 0.3, torch.bfloat16),
+    (64, 130, 1.0, torch.float16)])
+def test_bsa_fwd_matches_masked_dense(dev, d, length, density, pv):
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+    heads = 2
+    cfg = DfsConfig("t", (1, 1, length), heads, d, torch.bfloat16, seed=11)
+    q, k, v = synth_qkv(cfg)
+    nb = math.ceil(length / 128)
+    g = torch.Generator().manual_seed(12)
+    mask = torch.rand((heads, nb, nb), generator=g) < density
+    mask[:, torch.arange(nb), torch.arange(nb)] = True  # no empty rows
+    out = _run_bsa(dev, q, k, v, mask, pv, torch.float32)
+    ref = orc.masked_attention(q, k, v, mask)
+    max_abs = float((out - ref).abs().max())
+    mr = mean_rel(out, ref)
+    tol = 1e-3 if pv == torch.float16 else 3e-3  # bf16 P: reference-kernel precision class
+    assert max_abs <= 2e-2 and mr <= tol, (max_abs, mr)
+    if density == 1.0:
+        dense = orc.dense_attention(q, k, v)
+        assert mean_rel(out, dense) <= tol
+
+
+def test_bsa_fwd_bf16_out_and_fused_unpermute(dev):
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+    heads, d, length = 2, 128, 1000
+    cfg = DfsConfig("t", (1, 1, length), heads, d, torch.bfloat16, seed=13)
+    q, k, v = synth_qkv(cfg)
+    nb = math.ceil(length / 128)
+    mask = torch.rand((heads, nb, nb), generator=torch.Generator().manual_seed(2)) < 0.4
+    mask[:, :, 0] = True
+    perm = torch.randperm(length, generator=torch.Generator().manual_seed(3))
+    out32 = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32)
+    out16 = _run_bsa(dev, q, k, v, mask, torch.float16, torch.bfloat16)
+    assert torch.equal(out16, out32.to(torch.bfloat16))
+    scat = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32, perm=perm)
+    assert torch.equal(scat[:, :, perm], out32)
+
+
+def test_empty_rows_give_zero(dev):
+    heads, d, length = 1, 128, 512
+    q, k, v = (torch.randn((1, heads, length, d)).to(torch.bfloat16) for _ in range(3))
+    mask = torch.zeros((heads, 4, 4), dtype=torch.bool)
+    mask[0, 0, 1] = True
+    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32)
+    assert torch.count_nonzero(out[:, :, 128:]) == 0
+    ref = orc.masked_attention(q, k, v, mask)
+    assert mean_rel(out[:, :, :128], ref[:, :, :128]) < 1e-3

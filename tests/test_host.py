@@ -1,0 +1,109 @@
+"""Host-side logic and the C-ABI surface (CPU only: no kernel is launched)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from dfsattn_amd import _lib, ops
+from dfsattn_amd.layout import (ScoringLayout, TopkPolicy, csr_flops, block_flops, dense_policy,
+                                hunyuan_policy, topk_count, wan_policy)
+from oracle import dfs_oracle as orc
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "dfsattn_amd.h")
+
+
+def test_library_exports_every_declared_symbol():
+    text = open(HEADER).read()
+    declared = set(re.findall(r"^\s*(?:int|const char\*)\s+(dfs_\w+)\s*\(", text, flags=re.M))
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+    lib = _lib.lib()
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.dfs_abi_version() == _lib.ABI_VERSION
+
+
+@pytest.mark.parametrize("grid", [(4, 16, 16), (3, 5, 7), (1, 1, 1), (2, 3, 1), (21, 45, 80), (33, 45, 80)])
+def test_hilbert_c_matches_numpy_oracle(grid):
+    got = ops.hilbert3d_perm(*grid).numpy()
+    assert np.array_equal(got, orc.hilbert3d_perm(*grid))
+
+
+def test_abi_rejects_bad_arguments_without_launching():
+    fake = ctypes.c_void_p(16)
+    with pytest.raises(_lib.DfsKernelError, match="head_dim=96"):
+        _lib.call("dfs_prepare_qkv", fake, fake, fake, fake, 2, 1000, 96, 0, 1000, 16, 1,
+                  fake, fake, fake, None, None, None, None, None, None)
+    with pytest.raises(_lib.DfsKernelError, match="tile_size"):
+        _lib.call("dfs_prepare_qkv", fake, fake, fake, fake, 2, 1000, 128, 0, 1000, 24, 1,
+                  fake, fake, fake, None, None, None, None, None, None)
+    with pytest.raises(_lib.DfsKernelError, match="k_pick"):
+        _lib.call("dfs_topk_from_scores", fake, 2, 8, 8, 8, 8, 9, 8, 8, fake, fake, None, None)
+    with pytest.raises(_lib.DfsKernelError, match="f16 inputs"):
+        _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 0, 0.1, fake, 2,
+                  None, None, None)
+    with pytest.raises(_lib.DfsKernelError, match="row_bytes"):
+        _lib.call("dfs_permute_gather", fake, fake, fake, 1, 10, 10, 10, 3, None)
+    with pytest.raises(_lib.DfsKernelError, match="positive"):
+        _lib.call("dfs_hilbert3d_perm", 0, 4, 4, fake)
+
+
+def test_ops_refuse_cpu_tensors():
+    x = torch.zeros(1, 2, 128, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.permute_gather(x, torch.arange(128, dtype=torch.int32))
+
+
+def test_config_shapes_and_policies():
+    wan = ScoringLayout(75600, 75600, 16)
+    assert (wan.q_blocks, wan.rows, wan.q_tiles, wan.k_tiles) == (591, 75648, 4728, 4728)
+    pol = wan_policy(wan, 0.3)
+    assert (pol.k_pick, pol.n_cand, pol.dense_row) == (177, 591, 591)
+    assert pol.nnz(40) == 4184280
+    assert pol.row_ptr(2)[-1] == 2 * 591 * 177
+    hy = ScoringLayout(118800 + 256, 118800, 16)
+    assert (hy.q_blocks, hy.video_blocks, hy.q_tiles, hy.k_tiles) == (931, 929, 7432, 7448)
+    hp = hunyuan_policy(hy, 0.3)
+    assert (hp.scored_rows, hp.n_cand, hp.k_pick, hp.dense_col, hp.dense_row) == (929, 928, 276, 928, 928)
+    counts = hp.row_counts()
+    assert (counts[:928] == 279).all() and (counts[928:] == 931).all()
+    assert hp.nnz(24) == 6280920
+    # schedule sparsities 0.3 / 0.2 / 0.1 -> Wan top-k 177 / 118 / 59 (0.2 * 591 = 118.2)
+    assert [topk_count(s, 591) for s in (0.3, 0.2, 0.1)] == [177, 118, 59]
+    d = dense_policy(wan)
+    assert (d.row_counts() == 591).all()
+
+
+def test_policy_errors_follow_the_reference():
+    with pytest.raises(AssertionError):
+        hunyuan_policy(ScoringLayout(118800 + 256, 118800, 16), 0.002)
+    with pytest.raises(RuntimeError, match="tile view"):
+        ScoringLayout(129 + 127, 129, 16)  # 2 video blocks + 127 text tokens > 2 blocks
+    with pytest.raises(ValueError, match="block_size"):
+        ScoringLayout(1000, 1000, 16, block=64)
+    with pytest.raises(AssertionError, match="divisible"):
+        ScoringLayout(1000, 1000, 48)
+    with pytest.raises(RuntimeError, match="out of range"):
+        wan_policy(ScoringLayout(1000, 1000, 16), 1.5)
+
+
+def test_policy_row_counts_match_oracle_masks():
+    for seq, video, ratio in ((1000, 1000, 0.3), (1060, 1000, 0.5), (1000, 1000, 0.05), (3256, 3000, 0.2)):
+        lay = ScoringLayout(seq, video, 16)
+        pol = wan_policy(lay, ratio) if seq == video else hunyuan_policy(lay, ratio)
+        s = torch.rand(2, pol.scored_rows, pol.k_blocks)
+        m = orc.mask_from_scores_wan(s, ratio) if seq == video else orc.mask_from_scores_hunyuan(s, ratio, seq, video)
+        assert np.array_equal(m.sum(-1)[0].numpy(), pol.row_counts())
+
+
+def test_flop_counts_use_valid_token_blocks():
+    mask = np.ones((2, 3, 3), dtype=bool)
+    assert block_flops(mask, 300, 64) == 4 * 64 * 300 * 300 * 2
+    pol = wan_policy(ScoringLayout(300, 300, 16), 1.0)
+    ptr = pol.row_ptr(2)
+    cols = np.tile(np.arange(3), 6)
+    assert csr_flops(ptr, cols, 2, 300, 64) == block_flops(mask, 300, 64)
+    # cfg 1 nominal bound 35.10 TFLOP
+    assert abs(4 * 128 * 128 * 128 * 4184280 / 1e12 - 35.10) < 0.01

@@ -1,0 +1,155 @@
+"""Pins the CPU oracle against the reference's own known answers, closed forms
+and invariants (CPU only)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dfs_oracle as orc
+
+
+# ---- a4: schedule — the reference's known-answer test
+# (tests/test_flashinfer64_attention.py:122-144, dynamic ratio == native schedule)
+def test_schedule_known_answers_dynamic():
+    expected = {11: (False, 0.30), 12: (True, 0.30), 23: (False, 0.30), 24: (True, 0.20),
+                35: (False, 0.20), 36: (True, 0.10), 47: (False, 0.10), 48: (False, 0.10),
+                49: (False, 0.10)}
+    for step, (refresh, ratio) in expected.items():
+        got = orc.compute_cache_schedule(step, 12, 12, 0.30, 0.10)
+        assert got[0] == refresh
+        assert got[1] == pytest.approx(ratio)
+
+
+def test_schedule_known_answers_fixed_and_errors():
+    # dcrt = 0: refresh at every interval (tests/test_flashinfer64_attention.py:146-157)
+    for step in (12, 24, 36, 48):
+        assert orc.compute_cache_schedule(step, 12, 12, 0.195, 0.0) == (True, 0.195)
+    assert orc.compute_cache_schedule(13, 12, 12, 0.195, 0.0)[0] is False
+    with pytest.raises(ValueError):
+        orc.compute_cache_schedule(0, 12, 0, 0.3, 0.1)
+    # 0.3 / 0.1 == 2.9999999999999996 -> ceil 3 -> three refreshes
+    assert [s for s in range(50) if orc.compute_cache_schedule(s, 12, 12, 0.3, 0.1)[0]] == [12, 24, 36]
+
+
+# ---- a1: Hilbert order
+def test_hilbert_one_bit_is_inverse_gray_of_interleaved_bits():
+    # With one bit per axis the Hilbert index is the Gray-decoded string
+    # (x, y, z) with axis 0 most significant: a closed form of Skilling's algorithm.
+    pts = np.array([[x, y, z] for x in (0, 1) for y in (0, 1) for z in (0, 1)])
+    codes = orc.hilbert_encode(pts, 3, 1)
+    for (x, y, z), c in zip(pts, codes):
+        b2, b1, b0 = x, x ^ y, x ^ y ^ z
+        assert int(c) == (b2 << 2) | (b1 << 1) | b0
+    assert [int(c) for c in orc.hilbert_encode(np.array([[0, 0], [0, 1], [1, 1], [1, 0]]), 2, 1)] == [0, 1, 2, 3]
+
+
+@pytest.mark.parametrize("dims,bits", [(2, 3), (3, 2), (3, 3)])
+def test_hilbert_curve_invariants_on_full_cubes(dims, bits):
+    side = 1 << bits
+    grids = np.meshgrid(*[np.arange(side)] * dims, indexing="ij")
+    pts = np.stack([g.reshape(-1) for g in grids], axis=1)
+    codes = orc.hilbert_encode(pts, dims, bits).astype(np.int64)
+    assert sorted(codes.tolist()) == list(range(side ** dims))  # bijection onto [0, 2^(n b))
+    walk = pts[np.argsort(codes)]
+    assert (walk[0] == 0).all()  # starts at the origin
+    steps = np.abs(np.diff(walk, axis=0)).sum(axis=1)
+    assert (steps == 1).all()  # consecutive indices are unit-adjacent
+
+
+@pytest.mark.parametrize("grid", [(4, 16, 16), (3, 5, 7), (1, 1, 9), (21, 45, 80)])
+def test_hilbert3d_perm_is_a_permutation_with_local_steps(grid):
+    f, h, w = grid
+    perm = orc.hilbert3d_perm(f, h, w)
+    assert sorted(perm.tolist()) == list(range(f * h * w))
+    z, rem = np.divmod(perm, h * w)
+    y, x = np.divmod(rem, w)
+    steps = np.abs(np.diff(z)) + np.abs(np.diff(y)) + np.abs(np.diff(x))
+    assert np.median(steps) == 1  # locality of the curve on non-power-of-two grids
+
+
+# ---- a5/a6: scoring, brute force on a tiny input
+def _brute_block_scores(qp, kp, tile, block, video_len):
+    """Loop restatement of attention_wan.py:176-246 / attention_hyvideo.py:331-422."""
+    _, heads, seq_len, dim = qp.shape
+    vb, kb = math.ceil(video_len / block), math.ceil(seq_len / block)
+    layout = [None] * (kb * block)
+    for p in range(video_len):
+        layout[p] = p
+    for t in range(seq_len - video_len):
+        layout[vb * block + t] = video_len + t
+    out = torch.zeros(heads, vb, kb, dtype=torch.float64)
+    for h in range(heads):
+        def tile_mean(x, t):
+            acc = torch.zeros(dim, dtype=torch.float64)
+            for p in range(t * tile, (t + 1) * tile):
+                if layout[p] is not None:
+                    acc += x[0, h, layout[p]].double()
+            return acc / tile
+        qt = [tile_mean(qp, t) for t in range(vb * block // tile)]
+        kt = [tile_mean(kp, t) for t in range(kb * block // tile)]
+        for i, qi in enumerate(qt):
+            s = torch.stack([qi @ kj for kj in kt]) / math.sqrt(dim)
+            p = torch.exp(s - s.max())
+            p = p / p.sum()
+            for j in range(len(kt)):
+                out[h, i // (block // tile), j // (block // tile)] += p[j]
+    return out
+
+
+@pytest.mark.parametrize("seq,video,tile", [(300, 300, 16), (256, 256, 32), (290, 250, 16)])
+def test_block_scores_match_brute_force(seq, video, tile):
+    torch.manual_seed(0)
+    qp, kp = torch.randn(1, 2, seq, 8), torch.randn(1, 2, seq, 8)
+    got = orc.block_scores(qp, kp, tile, 128, None if seq == video else video)
+    ref = _brute_block_scores(qp, kp, tile, 128, video)
+    assert torch.allclose(got.double(), ref, rtol=1e-5, atol=1e-7)
+    assert torch.allclose(got.sum(-1).double(), torch.full_like(ref.sum(-1), 128 / tile), rtol=1e-5)
+
+
+def test_wan_mask_matches_torch_topk_on_tie_free_scores():
+    s = torch.rand(3, 40, 40, generator=torch.Generator().manual_seed(1))
+    for ratio in (0.05, 0.3, 0.5, 1.0):
+        k = orc.topk_count(ratio, 40)
+        assert torch.equal(orc.mask_from_scores_wan(s, ratio), orc.mask_from_scores_torch(s, k))
+        assert (orc.mask_from_scores_wan(s, ratio).sum(-1) == k).all()
+
+
+def test_tie_order_is_lower_column_first():
+    s = torch.tensor([[[1.0, 2.0, 2.0, 2.0, 0.5]]])
+    assert orc.select_topk(s, 2).tolist() == [[[False, True, True, False, False]]]
+    assert bool(orc.boundary_ties(s, 2).item()) and not bool(orc.boundary_ties(s, 3).item())
+
+
+def test_hunyuan_mask_policy():
+    # 931 blocks, dense_start 928 (cfg 2 shape), sparsity 0.3 -> k=279, video budget 276
+    s = torch.rand(2, 929, 931, generator=torch.Generator().manual_seed(2))
+    m = orc.mask_from_scores_hunyuan(s, 0.3, 118800 + 256, 118800)
+    assert m.shape == (2, 931, 931)
+    assert m[:, :928, 928:].all() and m[:, 928:].all()
+    assert (m[:, :928, :928].sum(-1) == 276).all()
+    assert torch.equal(m[:, :928, :928], orc.mask_from_scores_torch(s[:, :928, :928], 276))
+    with pytest.raises(AssertionError):
+        orc.mask_from_scores_hunyuan(s[:, :, :], 0.002, 118800 + 256, 118800)
+
+
+# ---- a8: masked attention
+def test_masked_attention_matches_dense_closed_form():
+    torch.manual_seed(3)
+    q, k, v = (torch.randn(1, 2, 300, 16) for _ in range(3))
+    mask = torch.rand(2, 3, 3) < 0.5
+    mask[:, :, 0] = True
+    got = orc.masked_attention(q, k, v, mask)
+    ref = orc.dense_attention(q, k, v, orc.expand_block_mask(mask, 300))
+    assert torch.allclose(got, ref, atol=1e-5)
+    full = torch.ones(2, 3, 3, dtype=torch.bool)
+    assert torch.allclose(orc.masked_attention(q, k, v, full), orc.dense_attention(q, k, v), atol=1e-5)
+
+
+def test_full_reference_call_is_permutation_consistent():
+    torch.manual_seed(4)
+    q, k, v = (torch.randn(1, 2, 256, 16) for _ in range(3))
+    perm = torch.from_numpy(orc.hilbert3d_perm(1, 16, 16))
+    out, mask, scores = orc.dfs_attention_reference(q, k, v, perm, 1.0, 16)
+    assert mask.all()
+    assert torch.allclose(out, orc.dense_attention(q, k, v), atol=1e-5)
