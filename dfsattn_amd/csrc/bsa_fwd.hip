@@ -160,7 +160,8 @@ __global__ void __launch_bounds__(256, 2)
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int64_t row = static_cast<int64_t>(h) * p.Qb + qb;
-  const int beg = row_ptr[row], end = row_ptr[row + 1];
+  const int beg = row_ptr[row];
+  const int end = beg + min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
   const int qrow = qb * 128 + w * 32 + l32;
 
   f32x16 o[DCH];
