@@ -1,0 +1,220 @@
+"""Benchmark of the DFS sparse-attention hot path on one MI355X.
+
+Workload: one DFS attention call at the Wan shape,
+B=1, 21x45x80 = 75,600 tokens, 40 heads, head_dim 128, bf16, tile 16, block
+128, hilbert3d order, sparsity 0.3, mask computed fresh every call. A step is
+one full call through the public entry point ``dfs_attention``: Hilbert gather
+of Q/K/V (+ tile pooling), block scoring + top-k, block-sparse attention with
+the fused inverse permutation.
+
+Prints one JSON line (metric = ms per call, lower is better) with the
+roofline of the attention kernel, per-phase kernel times and a CPU baseline
+(the fp32 oracle on a bounded sample of the same workload, scaled up).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/f16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def _events():
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def run_gpu(args):
+    from dfsattn_amd import ops
+    from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention, _dfs_attention_instances
+    from dfsattn_amd.layout import ScoringLayout, csr_flops, wan_policy
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[1]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("generating cfg1 inputs on the GPU")
+    q, k, v = synth_qkv(cfg, device=dev)
+    torch.cuda.synchronize()
+    log("inputs ready; warmup")
+    f, h, w = cfg.grid
+    video_perm = hilbert3d_perm(f, h, w)
+    L = cfg.seq_len
+
+    # One call per step, mask refreshed every call (step index at a refresh
+    # step with cache_flag=True; Wan counts CFG passes, so 2*skip_steps).
+    def step():
+        return dfs_attention(q, k, v, step_idx=0, skip_steps=0, cache_interval=1, layer_idx=0,
+                             sparsity=cfg.sparsity, sparsity_dcrt=0.0, tile_size=cfg.tile,
+                             block_size=cfg.block, video_perm=video_perm, cache_flag=True)
+
+    for i in range(args.warmup):
+        step()
+        torch.cuda.synchronize()
+        log(f"warmup step {i + 1}/{args.warmup} done")
+    t0 = time.perf_counter()
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(args.steps):
+        out = step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/call")
+
+    # Per-kernel times of the same call, each bracketed by events on the
+    # stream the kernels run on (the current stream), averaged over steps.
+    layout = ScoringLayout(L, L, cfg.tile)
+    pol = wan_policy(layout, cfg.sparsity)
+    perm_d = ops.device_perm(video_perm, dev)
+    row_ptr = torch.from_numpy(pol.row_ptr(cfg.heads)).to(dev)
+    reps = max(3, args.steps)
+    ev = {name: [] for name in ("prepare", "score_topk", "attention")}
+    for _ in range(reps):
+        a0, a1 = _events(); b1, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record()
+        prep = ops.prepare_qkv(q, k, v, perm_d, layout)
+        a1.record()
+        col_idx, _, _ = ops.block_score_topk(prep, pol, row_ptr)
+        b1.record()
+        ops.bsa_fwd(prep, row_ptr, col_idx, out_perm=perm_d)
+        c1.record()
+        torch.cuda.synchronize()
+        ev["prepare"].append(a0.elapsed_time(a1))
+        ev["score_topk"].append(a1.elapsed_time(b1))
+        ev["attention"].append(b1.elapsed_time(c1))
+    phase_ms = {k_: float(np.mean(v_)) for k_, v_ in ev.items()}
+    log(f"phase times (ms): {phase_ms}")
+    flops = csr_flops(row_ptr.cpu().numpy(), col_idx.cpu().numpy(), cfg.heads, L, cfg.head_dim)
+    att_tflops = flops / (phase_ms["attention"] * 1e-3) / 1e12
+    D = cfg.head_dim
+    tensor_bytes = cfg.heads * L * D * 2
+    prep_bytes = 3 * 2 * tensor_bytes  # read + write of Q, K, V (pooled outputs are ~1/16 extra)
+    score_flop = 2 * layout.q_tiles * layout.k_tiles * D * cfg.heads
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()
+    return {
+        "ms_per_step": ms_per_step,
+        "wall_ms_per_step": wall_ms,
+        "phase_ms": phase_ms,
+        "attention_flop": flops,
+        "attention_tflops": att_tflops,
+        "prepare_gbs": prep_bytes / (phase_ms["prepare"] * 1e-3) / 1e9,
+        "score_pooled_gflop": score_flop / 1e9,
+        "density": flops / (4.0 * D * L * L * cfg.heads),
+        "out_shape": list(out.shape),
+    }
+
+
+def cpu_baseline(time_budget_s: float = 20.0):
+    """fp32 oracle on the host cores on a bounded sample of the cfg-1 call:
+    scoring + top-k for 8 of 40 heads and masked attention for 96 query
+    blocks of 1 head, scaled linearly to the full call."""
+    from oracle import dfs_oracle as orc
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[1]
+    sample_heads = 8
+    sub = type(cfg)(cfg.name, cfg.grid, sample_heads, cfg.head_dim, torch.float32, seed=cfg.seed)
+    log(f"cpu baseline: generating {sample_heads} heads on the host")
+    q, k, v = synth_qkv(sub, device="cpu", dtype=torch.float32)
+    perm = torch.from_numpy(orc.hilbert3d_perm(*cfg.grid))
+    log("cpu baseline: scoring")
+    t0 = time.perf_counter()
+    qp, kp, vp = (orc.apply_permutation(x, perm) for x in (q, k, v))
+    scores = orc.block_scores(qp, kp, cfg.tile, cfg.block, None, head_chunk=1)
+    mask = orc.mask_from_scores_wan(scores, cfg.sparsity)
+    t_score = time.perf_counter() - t0
+    log(f"cpu baseline: scoring took {t_score:.1f} s; attention sample")
+    qblocks = list(range(0, 591, 6))[:96]
+    t1 = time.perf_counter()
+    orc.masked_attention(qp, kp, vp, mask, cfg.block, heads=[0], q_blocks=qblocks)
+    t_att = time.perf_counter() - t1
+    n_qb = math.ceil(cfg.seq_len / cfg.block)
+    full_s = t_score * cfg.heads / sample_heads + t_att * (cfg.heads * n_qb) / len(qblocks)
+    return {
+        "value": full_s * 1e3,
+        "unit": "ms/call",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"cfg1 fp32 oracle: permute+scoring+top-k of {sample_heads}/40 heads "
+                   f"({t_score:.1f} s, x{cfg.heads // sample_heads}) + masked attention of "
+                   f"{len(qblocks)}/{n_qb} query blocks of 1 head ({t_att:.1f} s, "
+                   f"x{cfg.heads * n_qb / len(qblocks):.0f})"),
+        "host": {"os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+                 "torch_threads": torch.get_num_threads(), "cpu_model": _cpu_model()},
+    }
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the DFS hot path is benchmarked on a single MI355X "
+              "(multi-GPU sharding by head is a design note, not part of this build).", file=sys.stderr)
+        sys.exit(2)
+    res = run_gpu(args)
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+    att_ms = res["phase_ms"]["attention"]
+    line = {
+        "metric": "DFS attn ms/call @75.6k tok,40h,d128 bf16; % bf16 MFMA peak on kept blocks",
+        "value": round(res["ms_per_step"], 3),
+        "unit": "ms/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (smoothed-field Q/K, iid V; seeded)",
+        "config": {"workload": "cfg1 Wan single DFS call: B=1, 21x45x80=75600 tokens, 40 heads, d128, "
+                               "tile 16, block 128, hilbert3d, sparsity 0.3, fresh mask per call",
+                   "global_batch": 1, "seq_len": 75600, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(res["attention_tflops"], 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(res["attention_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "bsa_fwd_kernel", "kernel_ms": round(att_ms, 3),
+                     "algorithmic_flop": res["attention_flop"]},
+        "phases_ms": {k_: round(v_, 3) for k_, v_ in res["phase_ms"].items()},
+        "prepare_gbs": round(res["prepare_gbs"], 1),
+        "kept_density": round(res["density"], 4),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -16,7 +16,6 @@ from dataclasses import dataclass
 from typing import Optional, Tuple
 
 import torch
-import torch.nn.functional as F
 
 
 @dataclass(frozen=True)
@@ -57,10 +56,14 @@ def _gauss_kernel(sigma: float) -> torch.Tensor:
 
 
 def _smooth_axis(x: torch.Tensor, kern: torch.Tensor, dim: int) -> torch.Tensor:
-    xm = x.movedim(dim, -1)
-    shape = xm.shape
-    y = F.conv1d(xm.reshape(-1, 1, shape[-1]), kern.view(1, 1, -1).to(x.device), padding=kern.numel() // 2)
-    return y.reshape(shape).movedim(-1, dim)
+    """Zero-boundary 'same' convolution along ``dim`` as a product with the
+    banded (symmetric) Toeplitz matrix of the kernel."""
+    n = x.shape[dim]
+    r = kern.numel() // 2
+    idx = torch.arange(n)
+    off = idx[None, :] - idx[:, None]
+    band = torch.where(off.abs() <= r, kern[(off + r).clamp(0, 2 * r)], torch.zeros(()))
+    return (x.movedim(dim, -1) @ band.to(x.device)).movedim(-1, dim)
 
 
 def smoothed_field(grid: Tuple[int, int, int], heads: int, dim: int, sigma: float,

@@ -1,0 +1,122 @@
+"""End-to-end parity of the reference-compatible API on the GPU:
+dfs_attention (Wan and HunyuanVideo variants) against the CPU oracle's whole
+call on the same (bf16-rounded) inputs, and the mask cache behaviour."""
+import pytest
+import torch
+
+from oracle import dfs_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(out, ref):
+    return float((out.double() - ref.double()).abs().mean() / ref.double().abs().mean())
+
+
+@pytest.fixture(autouse=True)
+def _clean():
+    from dfsattn_amd import attention_hyvideo as hy
+    from dfsattn_amd import attention_wan as wan
+    for mod in (wan, hy):
+        mod.DFS_Attention.clear_cache()
+        mod._dfs_attention_instances.clear()
+    yield
+
+
+def test_wan_cfg0_shape_matches_oracle(dev):
+    """configs[0] shape (1,024 tokens, 2 heads, d64, tile 16, sparsity 0.3),
+    run in bf16 on the GPU (the native kernel takes bf16/f16, like
+    block_sparse_attn); the oracle runs fp32 on the same bf16 values."""
+    from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[0]
+    q, k, v = synth_qkv(cfg, dtype=torch.bfloat16)
+    perm = hilbert3d_perm(*cfg.grid)
+    out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=24, skip_steps=12, cache_interval=12,
+                        layer_idx=3, sparsity=0.3, sparsity_dcrt=0.1, tile_size=16, video_perm=perm)
+    assert out.dtype == torch.bfloat16 and out.shape == q.shape
+    ref, ref_mask, ref_scores = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.3, 16)
+    entry = DFS_Attention._cached_metadata[(3, "native", 128, 16, 16)]
+    mask = entry["block_mask"].cpu()
+    assert mask.shape == ref_mask.shape
+    assert (mask == ref_mask).float().mean() > 0.99
+    # output against the oracle attention on the GPU's own mask (fp32 reference)
+    p, inv = orc.full_permutation(perm, q.shape[2])
+    ref_own = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
+    assert _rel(out.cpu(), ref_own) < 4e-3  # includes the bf16 rounding of the output (~1.4e-3)
+    assert float((out.cpu().float() - ref_own).abs().max()) < 2e-2
+
+
+def test_wan_cache_reuses_mask_across_steps(dev):
+    from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[0]
+    q, k, v = (x.to(dev) for x in synth_qkv(cfg, dtype=torch.bfloat16))
+    perm = hilbert3d_perm(*cfg.grid)
+    kw = dict(skip_steps=12, cache_interval=12, layer_idx=1, sparsity=0.3, sparsity_dcrt=0.1, tile_size=16,
+              video_perm=perm)
+    dfs_attention(q, k, v, step_idx=24, **kw)  # refresh (real step 12)
+    key = (1, "native", 128, 16, 16)
+    first = DFS_Attention._cached_metadata[key]["col_idx"].clone()
+    # uncond pass + later steps reuse the cached mask even for different inputs
+    q2 = torch.flip(q, dims=[2])
+    out_cached = dfs_attention(q2, k, v, step_idx=25, **kw)
+    assert torch.equal(DFS_Attention._cached_metadata[key]["col_idx"], first)
+    from dfsattn_amd import ops
+    from dfsattn_amd.layout import ScoringLayout
+    lay = ScoringLayout(q.shape[2], q.shape[2], 16)
+    pd = ops.device_perm(perm, dev)
+    prep = ops.prepare_qkv(q2, k, v, pd, lay, pool=False)
+    ent = DFS_Attention._cached_metadata[key]
+    direct = ops.bsa_fwd(prep, ent["row_ptr"], ent["col_idx"], out_perm=pd)
+    assert torch.equal(out_cached, direct)
+    # the next refresh (real step 24) recomputes with sparsity 0.2
+    dfs_attention(q2, k, v, step_idx=48, **kw)
+    assert DFS_Attention._cached_metadata[key]["policy"].k_pick == max(1, int(0.2 * 8))
+
+
+def test_hunyuan_with_text_matches_oracle(dev):
+    from dfsattn_amd.attention_hyvideo import DFS_Attention, dfs_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+
+    cfg = DfsConfig("hy-small", (3, 16, 20), 2, 128, torch.bfloat16, text_len=100, seed=9)
+    q, k, v = synth_qkv(cfg)
+    perm = hilbert3d_perm(*cfg.grid)
+    L, vl = cfg.seq_len, cfg.video_len
+    out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=12, skip_steps=12, cache_interval=12,
+                        layer_idx=0, sparsity=0.5, sparsity_dcrt=0.1, tile_size=16, video_len=vl,
+                        video_perm=perm)
+    ref, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.5, 16, video_len=vl)
+    key = next(iter(DFS_Attention._cached_metadata))
+    mask = DFS_Attention._cached_metadata[key]["block_mask"].cpu()
+    assert mask[:, :, vl // 128:].all() and mask[:, vl // 128:].all()
+    assert (mask == ref_mask).float().mean() > 0.99
+    p, inv = orc.full_permutation(perm, L)
+    ref_own = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
+    assert _rel(out.cpu(), ref_own) < 4e-3
+    # text query rows attend to everything: equal to dense attention there
+    dense = orc.dense_attention(q.float(), k.float(), v.float())
+    text_rows = out.cpu()[:, :, vl:].float()
+    assert _rel(text_rows, dense[:, :, vl:]) < 4e-3
+
+
+def test_api_rejects_what_the_native_path_cannot_run(dev):
+    from dfsattn_amd.attention_hyvideo import dfs_attention as hy_dfs
+    from dfsattn_amd.attention_wan import dfs_attention
+
+    q = torch.randn(1, 2, 256, 64, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        dfs_attention(q, q, q, step_idx=100, sparse_execution="hybrid", tile_size=16)
+    with pytest.raises(ValueError):
+        dfs_attention(q, q, q, step_idx=100, sparse_execution="flashinfer64")
+    with pytest.raises(RuntimeError):
+        dfs_attention(q.float(), q.float(), q.float(), step_idx=100, layer_idx=7, tile_size=16)
+    with pytest.raises(ValueError):
+        hy_dfs(q, q, q, step_idx=30, layer_idx=2, tile_size=16, video_len=200, block_top_p=0.9)
+    with pytest.raises(NotImplementedError):
+        hy_dfs(q, q, q, step_idx=30, layer_idx=3, tile_size=16, video_len=200, flashinfer64_valid_sequence=250)
