@@ -19,6 +19,7 @@
 // c ^ (r % 16) so the 32 rows read by one MFMA operand fetch hit distinct
 // banks.
 #include <math.h>
+#include <stdlib.h>
 
 #include "common.h"
 
@@ -27,6 +28,7 @@ namespace {
 
 struct BsaParams {
   int H, L, R, Qb, Kb;
+  int sched;  // workgroup order: 0 head-major across XCDs, 1 XCD-contiguous
   float scale_log2;
   int out_kind;  // 0 bf16, 1 f16, 2 f32
 };
@@ -107,28 +109,52 @@ __device__ __forceinline__ uint4 lds_chunk(const uint16_t* lds, int r, int c) {
   return *reinterpret_cast<const uint4*>(lds + (r * CPR + (c ^ (r % CPR))) * 8);
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
 template <bool F16>
 struct MfmaOp;
 template <>
 struct MfmaOp<false> {
   typedef bf16x8 vec;
+  typedef bf16x2 pair;
   static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t pack(float x, float y) {
-    return f32_to_bf16_bits(x) | (f32_to_bf16_bits(y) << 16);
+  // One v_cvt_pk (round to nearest even) per pair.
+  static __device__ __forceinline__ pair pack(float x, float y) {
+    return __builtin_convertvector((f32x2){x, y}, pair);
+  }
+  // acc + x.lo + x.hi in fp32 (v_dot2 with ones).
+  static __device__ __forceinline__ float sum2(pair x, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(x, (pair){(__bf16)1.0f, (__bf16)1.0f}, acc, false);
   }
 };
 template <>
 struct MfmaOp<true> {
   typedef f16x8 vec;
+  typedef f16x2 pair;
   static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t pack(float x, float y) {
-    return f32_to_f16_bits(x) | (f32_to_f16_bits(y) << 16);
+  static __device__ __forceinline__ pair pack(float x, float y) {
+    return __builtin_convertvector((f32x2){x, y}, pair);
+  }
+  static __device__ __forceinline__ float sum2(pair x, float acc) {
+    return __builtin_amdgcn_fdot2(x, (pair){(_Float16)1.0f, (_Float16)1.0f}, acc, false);
   }
 };
+
+// Value of the other lane half (lane ^ 32) combined with this lane's.
+__device__ __forceinline__ float xhalf_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 template <int D, bool QK_F16, bool PV_F16>
 __global__ void __launch_bounds__(256, 2)
@@ -150,13 +176,27 @@ __global__ void __launch_bounds__(256, 2)
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * 128];
   extern __shared__ int32_t cols[];  // kept key blocks of this row (dynamic)
 
-  // XCD-aware order: hardware deals workgroup b to XCD b % 8, so give each XCD
-  // a contiguous run of (head, query block) pairs; neighbouring query blocks
-  // keep mostly the same key blocks and share them in that XCD's L2.
-  const int nwg = gridDim.x, b = blockIdx.x;
-  const int xcd = b & 7, per = nwg >> 3, rem = nwg & 7;
-  const int id = xcd * per + min(xcd, rem) + (b >> 3);
-  const int h = id / p.Qb, qb = id - h * p.Qb;
+  // XCD-aware order. Hardware deals workgroup b to XCD b % 8 and each XCD runs
+  // its workgroups in increasing b. Head-major mode (default): the i-th
+  // workgroup of XCD x takes head i / S and query block x * S + i % S
+  // (S = ceil(Qb / 8)), so all eight XCDs sweep the same head together: one
+  // head's K/V (38.7 MB at 75.6k tokens) stays resident in the shared last-
+  // level cache while each XCD's L2 serves neighbouring query blocks, which
+  // keep mostly the same key blocks. Mode 1: each XCD owns a contiguous run
+  // of (head, query block) pairs instead.
+  int h, qb;
+  const int b = blockIdx.x, xcd = b & 7, i = b >> 3;
+  if (p.sched == 0) {
+    const int S = (p.Qb + 7) >> 3;
+    h = i / S;
+    qb = xcd * S + (i - h * S);
+    if (qb >= p.Qb) return;  // padding slot of the last XCD
+  } else {
+    const int nwg = gridDim.x, per = nwg >> 3, rem = nwg & 7;
+    const int id = xcd * per + min(xcd, rem) + i;
+    h = id / p.Qb;
+    qb = id - h * p.Qb;
+  }
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int64_t row = static_cast<int64_t>(h) * p.Qb + qb;
@@ -202,15 +242,23 @@ __global__ void __launch_bounds__(256, 2)
       wait_vmcnt<V_LOADS>();  // this wave's K copies have landed
       block_barrier();        // ... and everybody else's
 
+      // S^T = K Q^T; the LDS operands of the next 32-key chunk are fetched
+      // while the current chunk's MFMAs run.
       f32x16 s[4];
+      uint4 a[2][DS];
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) a[0][ds] = lds_chunk<CPR>(k_lds, l32, ds * 2 + hl);
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
+        if (kc + 1 < 4) {
+#pragma unroll
+          for (int ds = 0; ds < DS; ++ds)
+            a[(kc + 1) & 1][ds] = lds_chunk<CPR>(k_lds, (kc + 1) * 32 + l32, ds * 2 + hl);
+        }
         s[kc] = f32x16{};
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-          const uint4 a = lds_chunk<CPR>(k_lds, kc * 32 + l32, ds * 2 + hl);
-          s[kc] = QkOp::run(__builtin_bit_cast(typename QkOp::vec, a), qf[ds], s[kc]);
-        }
+        for (int ds = 0; ds < DS; ++ds)
+          s[kc] = QkOp::run(__builtin_bit_cast(typename QkOp::vec, a[kc & 1][ds]), qf[ds], s[kc]);
       }
       block_barrier();  // K tile fully consumed
       if (more) kcopy.template issue<K_LOADS>(krs, kb_next * TILE_BYTES, k_base, ws);
@@ -230,35 +278,33 @@ __global__ void __launch_bounds__(256, 2)
       for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kc][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(m, mx * p.scale_log2);
-      const float alpha = exp2_fast(m - mnew);
+      const float mnew = fmaxf(m, xhalf_max(mx) * p.scale_log2);
+      // Rescale only when some row's maximum moved (alpha == 1 otherwise).
+      if (__any(mnew > m)) {
+        const float alpha = exp2_fast(m - mnew);
+        lsum *= alpha;
+#pragma unroll
+        for (int i = 0; i < DCH; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+      }
       m = mnew;
-      float ps = 0.f;
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = exp2_fast(fmaf(s[kc][r], p.scale_log2, -mnew));
-          s[kc][r] = e;
-          ps += e;
-        }
-      lsum = fmaf(lsum, alpha, ps);
-#pragma unroll
-      for (int i = 0; i < DCH; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+      // P = exp2(S * scale * log2e - m), rounded to the PV operand type; the
+      // row sum accumulates the rounded values, so numerator and
+      // denominator of O = P V / sum(P) see the same P.
       typename PvOp::vec pf[8];
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
         const f32x16& src = s[ks >> 1];
         const int r0 = (ks & 1) * 8;
-        uint4 u;
-        u.x = PvOp::pack(src[r0 + 0], src[r0 + 1]);
-        u.y = PvOp::pack(src[r0 + 2], src[r0 + 3]);
-        u.z = PvOp::pack(src[r0 + 4], src[r0 + 5]);
-        u.w = PvOp::pack(src[r0 + 6], src[r0 + 7]);
-        pf[ks] = __builtin_bit_cast(typename PvOp::vec, u);
+        typename PvOp::pair pr[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          pr[j] = PvOp::pack(exp2_fast(fmaf(src[r0 + 2 * j], p.scale_log2, -mnew)),
+                             exp2_fast(fmaf(src[r0 + 2 * j + 1], p.scale_log2, -mnew)));
+          lsum = PvOp::sum2(pr[j], lsum);
+        }
+        pf[ks] = __builtin_bit_cast(typename PvOp::vec, pr);
       }
 
       if (more) wait_vmcnt<K_LOADS>(); else wait_vmcnt_0();  // V copies landed
@@ -277,7 +323,7 @@ __global__ void __launch_bounds__(256, 2)
   }
 
   // Epilogue: O = O^T / l, row qrow, columns d = dc*32 + g*8 + hl*4 + (0..3).
-  const float ltot = lsum + __shfl_xor(lsum, 32);
+  const float ltot = xhalf_sum(lsum);
   const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
   if (qrow >= p.L) return;
   const int orow = out_perm ? out_perm[qrow] : qrow;
@@ -316,7 +362,8 @@ struct BsaArgs {
 
 template <int D>
 void launch_bsa(const BsaArgs& a, const BsaParams& p, bool qk_f16, bool pv_f16, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>(p.H * p.Qb));
+  const int S = (p.Qb + 7) / 8;
+  dim3 grid(static_cast<unsigned>(p.sched == 0 ? 8 * S * p.H : p.H * p.Qb));
   const size_t smem = static_cast<size_t>(p.Kb) * sizeof(int32_t);
   if (qk_f16)
     bsa_fwd_kernel<D, true, true><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
@@ -364,6 +411,8 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   p.Kb = static_cast<int>(qb);
   p.scale_log2 = scale * 1.4426950408889634f;
   p.out_kind = out_dtype;
+  const char* sched = getenv("DFSATTN_AMD_BSA_SCHED");
+  p.sched = (sched && sched[0] == '1') ? 1 : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool qk_f16 = dtype == DFS_DTYPE_F16, pv_f16 = pv_dtype == DFS_DTYPE_F16;
   if (head_dim == 128)
