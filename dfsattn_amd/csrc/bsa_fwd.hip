@@ -3,17 +3,24 @@
 // dfsattn/attention_hyvideo.py:1075-1082).
 //
 // One workgroup = one (head, 128-row query block); four waves own 32 query
-// rows each. The workgroup walks the CSR list of kept 128-key blocks. Per
-// block, K (row-major) and V^T (transposed by the permute kernel) are copied
-// straight from global memory into LDS with 16-byte buffer loads, each in
-// its own buffer so the copy of the next K overlaps this block's softmax and
-// PV product, and the copy of the next V overlaps the next QK^T.
+// rows each and walk the CSR list of kept 128-key blocks. K (row-major) and
+// V^T (transposed by the permute kernel) tiles are copied straight from
+// global memory into LDS with 16-byte buffer loads.
 //
 // Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16 (lane column =
-// query, registers = keys), so row statistics of the online softmax need one
-// cross-half exchange only. P is rounded to f16 (or bf16) and multiplied with
-// V^T as O^T += V^T P^T; the accumulator register order of S^T is reused as
-// the token order of the PV operand, which the V^T layout matches.
+// query, registers = keys), so the online-softmax row statistics need one
+// exchange between the two lane halves only. P is rounded to f16 (or bf16)
+// and multiplied with V^T as O^T += V^T P^T; the register order of the S^T
+// accumulator is reused as the token order of the PV operand, which the V^T
+// layout matches.
+//
+// Two schedules:
+//  * pipelined: one workgroup per CU, 512 registers per wave, K and
+//    V double-buffered in LDS (128 KB). Iteration i computes QK^T of block
+//    i+1 next to the softmax of block i, then P V of block i; one barrier per
+//    block, and the copies of the next blocks overlap a whole iteration.
+//  * split (default): two workgroups per CU, single K and V buffers, four
+//    barriers per block; the other workgroup on the CU fills the gaps.
 //
 // LDS rows are 256 bytes; 16-byte chunk c of row r is stored at chunk
 // c ^ (r % 16) so the 32 rows read by one MFMA operand fetch hit distinct
@@ -28,7 +35,8 @@ namespace {
 
 struct BsaParams {
   int H, L, R, Qb, Kb;
-  int sched;  // workgroup order: 0 head-major across XCDs, 1 XCD-contiguous
+  int sched;   // workgroup order: 0 head-major across XCDs, 1 XCD-contiguous
+  int rotate;  // rotated key-block sweep (split schedule)
   float scale_log2;
   int out_kind;  // 0 bf16, 1 f16, 2 f32
 };
@@ -62,7 +70,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 // 16 bytes per lane from buffer offset voff + soff into LDS at m0 + 16 * lane.
 // Issued as inline assembly so the compiler does not serialise every later LDS
-// read behind it; the kernel waits for these loads with explicit vmcnt counts
+// read behind it; the kernels wait for these loads with explicit vmcnt counts
 // (the compiler's own vmcnt waits stay correct, only more conservative). The
 // asm is volatile, so it keeps its place relative to the barrier asm (which
 // carries the memory clobber that orders the LDS reads).
@@ -156,173 +164,127 @@ __device__ __forceinline__ float xhalf_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int D, bool QK_F16, bool PV_F16>
-__global__ void __launch_bounds__(256, 2)
-    bsa_fwd_kernel(const uint16_t* __restrict__ q,        // [H][R][D]
-                   const uint16_t* __restrict__ k,        // [H][R][D]
-                   const uint16_t* __restrict__ vt,       // [H][R/128][D][128]
-                   const int32_t* __restrict__ row_ptr,   // [H*Qb+1]
-                   const int32_t* __restrict__ col_idx,   // CSR columns
-                   void* __restrict__ out, const int32_t* __restrict__ out_perm,
-                   float* __restrict__ lse, BsaParams p) {
-  constexpr int CPR = D / 8;       // 16-byte chunks per K row
-  constexpr int DS = D / 16;       // QK^T k-steps
-  constexpr int DCH = D / 32;      // 32-row chunks of O^T
-  constexpr int K_LOADS = CPR / 2; // global_load_lds per thread for a K tile
-  constexpr int V_LOADS = D / 16;  // ... for a V^T tile (D rows x 256 bytes)
-  typedef MfmaOp<QK_F16> QkOp;
-  typedef MfmaOp<PV_F16> PvOp;
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[128 * D];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * 128];
-  extern __shared__ int32_t cols[];  // kept key blocks of this row (dynamic)
-
-  // XCD-aware order. Hardware deals workgroup b to XCD b % 8 and each XCD runs
-  // its workgroups in increasing b. Head-major mode (default): the i-th
-  // workgroup of XCD x takes head i / S and query block x * S + i % S
-  // (S = ceil(Qb / 8)), so all eight XCDs sweep the same head together: one
-  // head's K/V (38.7 MB at 75.6k tokens) stays resident in the shared last-
-  // level cache while each XCD's L2 serves neighbouring query blocks, which
-  // keep mostly the same key blocks. Mode 1: each XCD owns a contiguous run
-  // of (head, query block) pairs instead.
-  int h, qb;
+// (head, query block) of this workgroup; false for a padding slot.
+// Hardware deals workgroup b to XCD b % 8 and each XCD runs its workgroups in
+// increasing b. Head-major mode (default): the i-th workgroup of XCD x takes
+// head i / S and query block x * S + i % S (S = ceil(Qb / 8)), so all eight
+// XCDs sweep the same head together: one head's K/V (38.7 MB at 75.6k tokens)
+// stays resident in the shared last-level cache while each XCD's L2 serves
+// neighbouring query blocks. Mode 1: each XCD owns a contiguous run of
+// (head, query block) pairs instead.
+__device__ __forceinline__ bool wg_coords(const BsaParams& p, int& h, int& qb) {
   const int b = blockIdx.x, xcd = b & 7, i = b >> 3;
   if (p.sched == 0) {
     const int S = (p.Qb + 7) >> 3;
     h = i / S;
     qb = xcd * S + (i - h * S);
-    if (qb >= p.Qb) return;  // padding slot of the last XCD
-  } else {
-    const int nwg = gridDim.x, per = nwg >> 3, rem = nwg & 7;
-    const int id = xcd * per + min(xcd, rem) + i;
-    h = id / p.Qb;
-    qb = id - h * p.Qb;
+    return qb < p.Qb;
   }
+  const int nwg = gridDim.x, per = nwg >> 3, rem = nwg & 7;
+  const int id = xcd * per + min(xcd, rem) + i;
+  h = id / p.Qb;
+  qb = id - h * p.Qb;
+  return true;
+}
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int64_t row = static_cast<int64_t>(h) * p.Qb + qb;
-  const int beg = row_ptr[row];
-  const int end = beg + min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
-  const int qrow = qb * 128 + w * 32 + l32;
-
-  f32x16 o[DCH];
+template <int D, typename QkOp>
+__device__ __forceinline__ void load_q(const uint16_t* __restrict__ q, const BsaParams& p, int h, int qrow,
+                                       int hl, typename QkOp::vec* qf) {
+  const uint4* src = reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(h) * p.R + qrow) * D);
 #pragma unroll
-  for (int i = 0; i < DCH; ++i) o[i] = f32x16{};
-  float m = -INFINITY, lsum = 0.f;
+  for (int s = 0; s < D / 16; ++s) qf[s] = __builtin_bit_cast(typename QkOp::vec, src[2 * s + hl]);
+}
 
-  if (beg < end) {
-    // Per-head buffer resources: K rows [R][D], V^T blocks [R/128][D][128].
-    const uint32_t head_bytes = static_cast<uint32_t>(p.R) * D * 2;
-    const sgpr4 krs = make_rsrc(k + static_cast<int64_t>(h) * p.R * D, head_bytes);
-    const sgpr4 vrs = make_rsrc(vt + static_cast<int64_t>(h) * p.R * D, head_bytes);
-    const uint32_t k_base = lds_addr(k_lds), v_base = lds_addr(v_lds);
-    const int ws = __builtin_amdgcn_readfirstlane(w);
-    const TileCopy<D * 2> kcopy(ws, lane);
-    const TileCopy<256> vcopy(ws, lane);
-    constexpr uint32_t TILE_BYTES = 128 * D * 2;
-    typename QkOp::vec qf[DS];
-    {
-      const uint4* qsrc = reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(h) * p.R + qrow) * D);
+// S^T (128 keys x this wave's 32 queries) = K Q^T from an LDS K tile; the
+// operands of the next 32-key chunk are fetched while this chunk's MFMAs run.
+template <int D, typename QkOp>
+__device__ __forceinline__ void qk_tile(const uint16_t* k_tile, const typename QkOp::vec* qf, int l32, int hl,
+                                        f32x16* s) {
+  constexpr int CPR = D / 8, DS = D / 16;
+  uint4 a[2][DS];
 #pragma unroll
-      for (int s = 0; s < DS; ++s) qf[s] = __builtin_bit_cast(typename QkOp::vec, qsrc[2 * s + hl]);
+  for (int ds = 0; ds < DS; ++ds) a[0][ds] = lds_chunk<CPR>(k_tile, l32, ds * 2 + hl);
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc) {
+    if (kc + 1 < 4) {
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) a[(kc + 1) & 1][ds] = lds_chunk<CPR>(k_tile, (kc + 1) * 32 + l32, ds * 2 + hl);
     }
-    // Column list of this row into LDS (read back with uniform ds_reads), and
-    // Q fragments forced complete here so no wait for them lands in the loop.
-    for (int i = tid; i < end - beg; i += 256) cols[i] = col_idx[beg + i];
+    s[kc] = f32x16{};
 #pragma unroll
-    for (int s = 0; s < DS; ++s) asm volatile("" ::"v"(qf[s]));
-    block_barrier();
-    int kb = cols[0];
-    kcopy.template issue<K_LOADS>(krs, kb * TILE_BYTES, k_base, ws);
-    vcopy.template issue<V_LOADS>(vrs, kb * TILE_BYTES, v_base, ws);
-    const bool tail_possible = (p.L & 127) != 0;
+    for (int ds = 0; ds < DS; ++ds)
+      s[kc] = QkOp::run(__builtin_bit_cast(typename QkOp::vec, a[kc & 1][ds]), qf[ds], s[kc]);
+  }
+}
 
-    for (int it = beg; it < end; ++it) {
-      const bool more = it + 1 < end;
-      const int kb_next = more ? __builtin_amdgcn_readfirstlane(cols[it + 1 - beg]) : 0;
-      wait_vmcnt<V_LOADS>();  // this wave's K copies have landed
-      block_barrier();        // ... and everybody else's
+// Keys >= valid of the block get -inf (only the last block can be partial).
+__device__ __forceinline__ void mask_tail(f32x16* s, int valid, int hl) {
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (kc * 32 + (r >> 2) * 8 + hl * 4 + (r & 3) >= valid) s[kc][r] = -INFINITY;
+}
 
-      // S^T = K Q^T; the LDS operands of the next 32-key chunk are fetched
-      // while the current chunk's MFMAs run.
-      f32x16 s[4];
-      uint4 a[2][DS];
+// Online-softmax bookkeeping of one block: returns the new running maximum
+// (log2 domain) and rescales O and l by exp2(m_old - m_new). With LAZY the
+// rescale is skipped when no row's maximum moved (alpha == 1 exactly).
+template <int DCH, bool LAZY>
+__device__ __forceinline__ float softmax_max(const f32x16* s, float scale_log2, float& m, float& lsum,
+                                             f32x16* o) {
+  float mx = -INFINITY;
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds) a[0][ds] = lds_chunk<CPR>(k_lds, l32, ds * 2 + hl);
+  for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        if (kc + 1 < 4) {
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kc][r]);
+  const float mnew = fmaxf(m, xhalf_max(mx) * scale_log2);
+  if (!LAZY || __any(mnew > m)) {
+    const float alpha = exp2_fast(m - mnew);
+    lsum *= alpha;
 #pragma unroll
-          for (int ds = 0; ds < DS; ++ds)
-            a[(kc + 1) & 1][ds] = lds_chunk<CPR>(k_lds, (kc + 1) * 32 + l32, ds * 2 + hl);
-        }
-        s[kc] = f32x16{};
+    for (int i = 0; i < DCH; ++i)
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds)
-          s[kc] = QkOp::run(__builtin_bit_cast(typename QkOp::vec, a[kc & 1][ds]), qf[ds], s[kc]);
-      }
-      block_barrier();  // K tile fully consumed
-      if (more) kcopy.template issue<K_LOADS>(krs, kb_next * TILE_BYTES, k_base, ws);
+      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+  }
+  m = mnew;
+  return mnew;
+}
 
-      // Online softmax in the log2 domain; lane column = query row.
-      if (tail_possible && kb == p.Kb - 1) {
-        int valid = p.L - kb * 128;
-        asm volatile("" : "+s"(valid));  // compares stay in this (rare) branch
+// O^T += V^T P^T, 16 keys per step. P = exp2(S * scale * log2e - m) is formed
+// step by step so its VALU work runs under the previous step's MFMAs; it is
+// rounded to the PV operand type and the row sum accumulates the rounded
+// values (numerator and denominator of O = P V / sum(P) see the same P).
+template <int D, typename PvOp>
+__device__ __forceinline__ void pv_tile(const uint16_t* v_tile, const f32x16* s, float scale_log2, float mnew,
+                                        float& lsum, f32x16* o, int l32, int hl) {
+  constexpr int DCH = D / 32;
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc)
+  for (int ks = 0; ks < 8; ++ks) {
+    const f32x16& src = s[ks >> 1];
+    const int r0 = (ks & 1) * 8;
+    typename PvOp::pair pr[4];
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (kc * 32 + (r >> 2) * 8 + hl * 4 + (r & 3) >= valid) s[kc][r] = -INFINITY;
-      }
-      float mx = -INFINITY;
+    for (int j = 0; j < 4; ++j) {
+      pr[j] = PvOp::pack(exp2_fast(fmaf(src[r0 + 2 * j], scale_log2, -mnew)),
+                         exp2_fast(fmaf(src[r0 + 2 * j + 1], scale_log2, -mnew)));
+      lsum = PvOp::sum2(pr[j], lsum);
+    }
+    const typename PvOp::vec pf = __builtin_bit_cast(typename PvOp::vec, pr);
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kc][r]);
-      const float mnew = fmaxf(m, xhalf_max(mx) * p.scale_log2);
-      // Rescale only when some row's maximum moved (alpha == 1 otherwise).
-      if (__any(mnew > m)) {
-        const float alpha = exp2_fast(m - mnew);
-        lsum *= alpha;
-#pragma unroll
-        for (int i = 0; i < DCH; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-      }
-      m = mnew;
-      // P = exp2(S * scale * log2e - m), rounded to the PV operand type; the
-      // row sum accumulates the rounded values, so numerator and
-      // denominator of O = P V / sum(P) see the same P.
-      typename PvOp::vec pf[8];
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        const f32x16& src = s[ks >> 1];
-        const int r0 = (ks & 1) * 8;
-        typename PvOp::pair pr[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          pr[j] = PvOp::pack(exp2_fast(fmaf(src[r0 + 2 * j], p.scale_log2, -mnew)),
-                             exp2_fast(fmaf(src[r0 + 2 * j + 1], p.scale_log2, -mnew)));
-          lsum = PvOp::sum2(pr[j], lsum);
-        }
-        pf[ks] = __builtin_bit_cast(typename PvOp::vec, pr);
-      }
-
-      if (more) wait_vmcnt<K_LOADS>(); else wait_vmcnt_0();  // V copies landed
-      block_barrier();
-#pragma unroll
-      for (int dc = 0; dc < DCH; ++dc)
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-          const uint4 a = lds_chunk<16>(v_lds, dc * 32 + l32, ks * 2 + hl);
-          o[dc] = PvOp::run(__builtin_bit_cast(typename PvOp::vec, a), pf[ks], o[dc]);
-        }
-      block_barrier();  // V tile fully consumed
-      if (more) vcopy.template issue<V_LOADS>(vrs, kb_next * TILE_BYTES, v_base, ws);
-      kb = kb_next;
+    for (int dc = 0; dc < DCH; ++dc) {
+      const uint4 a = lds_chunk<16>(v_tile, dc * 32 + l32, ks * 2 + hl);
+      o[dc] = PvOp::run(__builtin_bit_cast(typename PvOp::vec, a), pf, o[dc]);
     }
   }
+}
 
-  // Epilogue: O = O^T / l, row qrow, columns d = dc*32 + g*8 + hl*4 + (0..3).
+// O = O^T / l for row qrow, columns d = dc*32 + g*8 + hl*4 + (0..3); rows past
+// L are dropped, rows with no kept block give 0.
+template <int D>
+__device__ __forceinline__ void store_out(const BsaParams& p, void* __restrict__ out,
+                                          const int32_t* __restrict__ out_perm, float* __restrict__ lse,
+                                          const f32x16* o, float m, float lsum, int h, int qrow, int hl) {
+  constexpr int DCH = D / 32;
   const float ltot = xhalf_sum(lsum);
   const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
   if (qrow >= p.L) return;
@@ -348,8 +310,225 @@ __global__ void __launch_bounds__(256, 2)
       }
     }
   if (lse && hl == 0)
-    lse[static_cast<int64_t>(h) * p.L + qrow] =
-        ltot > 0.f ? (m + log2f(ltot)) * 0.69314718055994531f : -INFINITY;
+    lse[static_cast<int64_t>(h) * p.L + qrow] = ltot > 0.f ? (m + log2f(ltot)) * 0.69314718055994531f : -INFINITY;
+}
+
+#define BSA_KERNEL_ARGS                                                                                \
+  const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ vt,    \
+      const int32_t *__restrict__ row_ptr, const int32_t *__restrict__ col_idx, void *__restrict__ out, \
+      const int32_t *__restrict__ out_perm, float *__restrict__ lse, BsaParams p
+
+// Split schedule: two workgroups per CU, single K and V buffers.
+template <int D, bool QK_F16, bool PV_F16>
+__global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) {
+  constexpr int DCH = D / 32;
+  constexpr int K_LOADS = D / 16;  // buffer loads per thread for a K tile
+  constexpr int V_LOADS = D / 16;  // ... for a V^T tile (D rows x 256 bytes)
+  constexpr uint32_t TILE_BYTES = 128 * D * 2;
+  typedef MfmaOp<QK_F16> QkOp;
+  typedef MfmaOp<PV_F16> PvOp;
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[128 * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * 128];
+  extern __shared__ int32_t cols[];  // kept key blocks of this row (dynamic)
+
+  int h, qb;
+  if (!wg_coords(p, h, qb)) return;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int64_t row = static_cast<int64_t>(h) * p.Qb + qb;
+  const int beg = row_ptr[row];
+  const int end = beg + min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
+  const int qrow = qb * 128 + w * 32 + l32;
+
+  f32x16 o[DCH];
+#pragma unroll
+  for (int i = 0; i < DCH; ++i) o[i] = f32x16{};
+  float m = -INFINITY, lsum = 0.f;
+
+  if (beg < end) {
+    const uint32_t head_bytes = static_cast<uint32_t>(p.R) * D * 2;
+    const sgpr4 krs = make_rsrc(k + static_cast<int64_t>(h) * p.R * D, head_bytes);
+    const sgpr4 vrs = make_rsrc(vt + static_cast<int64_t>(h) * p.R * D, head_bytes);
+    const uint32_t k_base = lds_addr(k_lds), v_base = lds_addr(v_lds);
+    const int ws = __builtin_amdgcn_readfirstlane(w);
+    const TileCopy<D * 2> kcopy(ws, lane);
+    const TileCopy<256> vcopy(ws, lane);
+    typename QkOp::vec qf[D / 16];
+    load_q<D, QkOp>(q, p, h, qrow, hl, qf);
+    // Column list of this row into LDS (read back with uniform ds_reads), and
+    // Q fragments forced complete here so no wait for them lands in the loop.
+    for (int i = tid; i < end - beg; i += 256) cols[i] = col_idx[beg + i];
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qf[s]));
+    block_barrier();
+    const int n = end - beg;
+    // Rotated sweep: the i-th workgroup of an XCD starts at the first kept
+    // column >= i * Kb / CONC (CONC = workgroups resident per XCD) and wraps
+    // around. Workgroups start 1 / CONC of a sweep apart, so at any moment the
+    // resident workgroups of an XCD work on neighbouring key blocks and share
+    // them in L2. The order is a fixed function of the workgroup, so results
+    // are deterministic.
+    int j0 = 0;
+    if (p.rotate) {
+      constexpr int CONC = 64;  // 32 CUs per XCD x 2 workgroups per CU
+      const int start = static_cast<int>((static_cast<int64_t>(blockIdx.x >> 3) * p.Kb / CONC) % p.Kb);
+      int lo = 0, hi = n;  // lower_bound(cols, start)
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (cols[mid] < start) lo = mid + 1; else hi = mid;
+      }
+      j0 = lo == n ? 0 : lo;
+    }
+    auto col_at = [&](int t) -> int {
+      int j = j0 + t;
+      j = j >= n ? j - n : j;
+      return __builtin_amdgcn_readfirstlane(cols[j]);
+    };
+    int kb = col_at(0);
+    kcopy.template issue<K_LOADS>(krs, kb * TILE_BYTES, k_base, ws);
+    vcopy.template issue<V_LOADS>(vrs, kb * TILE_BYTES, v_base, ws);
+    const bool tail_possible = (p.L & 127) != 0;
+
+    for (int t = 0; t < n; ++t) {
+      // Past the last block the copies target a block beyond the buffer:
+      // out-of-range buffer loads return zero and fetch nothing, so every
+      // iteration issues the same number of loads and the waits stay fixed.
+      const int kb_next = t + 1 < n ? col_at(t + 1) : p.Kb;
+      wait_vmcnt<V_LOADS>();  // this wave's K copies have landed
+      block_barrier();        // ... and everybody else's
+      f32x16 s[4];
+      qk_tile<D, QkOp>(k_lds, qf, l32, hl, s);
+      block_barrier();  // K tile fully consumed
+      kcopy.template issue<K_LOADS>(krs, kb_next * TILE_BYTES, k_base, ws);
+      if (tail_possible && kb == p.Kb - 1) {
+        int valid = p.L - kb * 128;
+        asm volatile("" : "+s"(valid));  // compares stay in this (rare) branch
+        mask_tail(s, valid, hl);
+      }
+      const float mnew = softmax_max<DCH, true>(s, p.scale_log2, m, lsum, o);
+      wait_vmcnt<K_LOADS>();  // V copies landed (the next K may be in flight)
+      block_barrier();
+      pv_tile<D, PvOp>(v_lds, s, p.scale_log2, mnew, lsum, o, l32, hl);
+      block_barrier();  // V tile fully consumed
+      vcopy.template issue<V_LOADS>(vrs, kb_next * TILE_BYTES, v_base, ws);
+      kb = kb_next;
+    }
+    wait_vmcnt_0();  // the trailing (empty) copies have retired
+  }
+  store_out<D>(p, out, out_perm, lse, o, m, lsum, h, qrow, hl);
+}
+
+template <int V>
+struct Parity {
+  static constexpr int value = V;
+};
+
+// Pipelined schedule: one workgroup per CU (512 registers per wave), K and V
+// double-buffered. Block j lives in buffer j % 2. Iteration i: wait for the
+// copies issued one iteration earlier (K of block i+1, V of block i), barrier
+// (everybody finished iteration i-1, so K buffer i%2 and V buffer (i+1)%2 are
+// free), issue K of block i+2 and V of block i+1, then QK^T of block i+1
+// beside the softmax of block i, then P V of block i. Columns are ascending,
+// so only the last block can be the partial tail block; it is handled by the
+// peeled final iteration.
+template <int D, bool QK_F16, bool PV_F16>
+__global__ void __launch_bounds__(256, 1) bsa_fwd_pipe_kernel(BSA_KERNEL_ARGS) {
+  constexpr int DCH = D / 32;
+  constexpr int K_LOADS = D / 16;
+  constexpr int V_LOADS = D / 16;
+  constexpr uint32_t TILE_BYTES = 128 * D * 2;
+  constexpr int TILE = 128 * D;  // uint16 elements per tile
+  typedef MfmaOp<QK_F16> QkOp;
+  typedef MfmaOp<PV_F16> PvOp;
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2 * TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2 * TILE];
+  extern __shared__ int32_t cols[];
+
+  int h, qb;
+  if (!wg_coords(p, h, qb)) return;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int64_t row = static_cast<int64_t>(h) * p.Qb + qb;
+  const int beg = row_ptr[row];
+  const int n = min(max(row_ptr[row + 1] - beg, 0), p.Kb);
+  const int qrow = qb * 128 + w * 32 + l32;
+
+  f32x16 o[DCH];
+#pragma unroll
+  for (int i = 0; i < DCH; ++i) o[i] = f32x16{};
+  float m = -INFINITY, lsum = 0.f;
+
+  if (n > 0) {
+    const uint32_t head_bytes = static_cast<uint32_t>(p.R) * D * 2;
+    const sgpr4 krs = make_rsrc(k + static_cast<int64_t>(h) * p.R * D, head_bytes);
+    const sgpr4 vrs = make_rsrc(vt + static_cast<int64_t>(h) * p.R * D, head_bytes);
+    const uint32_t k_base = lds_addr(k_lds), v_base = lds_addr(v_lds);
+    const int ws = __builtin_amdgcn_readfirstlane(w);
+    const TileCopy<D * 2> kcopy(ws, lane);
+    const TileCopy<256> vcopy(ws, lane);
+    typename QkOp::vec qf[D / 16];
+    load_q<D, QkOp>(q, p, h, qrow, hl, qf);
+    for (int i = tid; i < n; i += 256) cols[i] = col_idx[beg + i];
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qf[s]));
+    block_barrier();
+    // Column of block j, or the out-of-range sentinel Kb past the end (its
+    // copies fetch nothing), so every iteration issues the same loads.
+    auto col = [&](int j) -> int {
+      const int c = __builtin_amdgcn_readfirstlane(cols[min(j, n - 1)]);
+      return j < n ? c : p.Kb;
+    };
+
+    // Prologue: K of blocks 0 and 1, V of block 0; QK^T of block 0.
+    kcopy.template issue<K_LOADS>(krs, col(0) * TILE_BYTES, k_base, ws);
+    kcopy.template issue<K_LOADS>(krs, col(1) * TILE_BYTES, k_base + TILE_BYTES, ws);
+    vcopy.template issue<V_LOADS>(vrs, col(0) * TILE_BYTES, v_base, ws);
+    wait_vmcnt_0();
+    block_barrier();
+    f32x16 sa[4], sb[4];
+    qk_tile<D, QkOp>(k_lds, qf, l32, hl, sa);
+
+    // One steady-state iteration with compile-time buffer parity PAR (= i % 2).
+    auto step = [&](int i, f32x16* s_cur, f32x16* s_next, auto par_tag) {
+      constexpr int PAR = decltype(par_tag)::value;
+      wait_vmcnt_0();  // K of block i+1, V of block i
+      block_barrier();
+      kcopy.template issue<K_LOADS>(krs, col(i + 2) * TILE_BYTES, k_base + PAR * TILE_BYTES, ws);
+      vcopy.template issue<V_LOADS>(vrs, col(i + 1) * TILE_BYTES, v_base + (1 - PAR) * TILE_BYTES, ws);
+      qk_tile<D, QkOp>(k_lds + (1 - PAR) * TILE, qf, l32, hl, s_next);
+      const float mnew = softmax_max<DCH, false>(s_cur, p.scale_log2, m, lsum, o);
+      pv_tile<D, PvOp>(v_lds + PAR * TILE, s_cur, p.scale_log2, mnew, lsum, o, l32, hl);
+      // Interleave: LDS operand reads run ahead, every MFMA is followed by the
+      // next read and a few VALU instructions (softmax of this block).
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int g = 0; g < 64; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      }
+    };
+    int i = 0;
+    for (; i + 2 < n; i += 2) {
+      step(i, sa, sb, Parity<0>{});
+      step(i + 1, sb, sa, Parity<1>{});
+    }
+    // One or two blocks remain; the last one may be the partial tail block.
+    auto last = [&](int j, f32x16* s_cur, auto par_tag) {
+      constexpr int PAR = decltype(par_tag)::value;
+      wait_vmcnt_0();  // V of block j
+      block_barrier();
+      const int kb = col(j);
+      if ((p.L & 127) != 0 && kb == p.Kb - 1) mask_tail(s_cur, p.L - kb * 128, hl);
+      const float mnew = softmax_max<DCH, false>(s_cur, p.scale_log2, m, lsum, o);
+      pv_tile<D, PvOp>(v_lds + PAR * TILE, s_cur, p.scale_log2, mnew, lsum, o, l32, hl);
+    };
+    if (i + 1 < n) {
+      step(i, sa, sb, Parity<0>{});
+      last(i + 1, sb, Parity<1>{});
+    } else {
+      last(i, sa, Parity<0>{});
+    }
+  }
+  store_out<D>(p, out, out_perm, lse, o, m, lsum, h, qrow, hl);
 }
 
 struct BsaArgs {
@@ -360,20 +539,27 @@ struct BsaArgs {
   float* lse;
 };
 
-template <int D>
-void launch_bsa(const BsaArgs& a, const BsaParams& p, bool qk_f16, bool pv_f16, hipStream_t s) {
+template <int D, bool QK_F16, bool PV_F16>
+void launch_typed(const BsaArgs& a, const BsaParams& p, bool pipelined, hipStream_t s) {
   const int S = (p.Qb + 7) / 8;
   dim3 grid(static_cast<unsigned>(p.sched == 0 ? 8 * S * p.H : p.H * p.Qb));
   const size_t smem = static_cast<size_t>(p.Kb) * sizeof(int32_t);
-  if (qk_f16)
-    bsa_fwd_kernel<D, true, true><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
-                                                        a.out_perm, a.lse, p);
-  else if (pv_f16)
-    bsa_fwd_kernel<D, false, true><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
-                                                         a.out_perm, a.lse, p);
+  if (pipelined)
+    bsa_fwd_pipe_kernel<D, QK_F16, PV_F16><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
+                                                                  a.out_perm, a.lse, p);
   else
-    bsa_fwd_kernel<D, false, false><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
-                                                          a.out_perm, a.lse, p);
+    bsa_fwd_split_kernel<D, QK_F16, PV_F16><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
+                                                                   a.out_perm, a.lse, p);
+}
+
+template <int D>
+void launch_bsa(const BsaArgs& a, const BsaParams& p, bool qk_f16, bool pv_f16, bool pipelined, hipStream_t s) {
+  if (qk_f16)
+    launch_typed<D, true, true>(a, p, pipelined, s);
+  else if (pv_f16)
+    launch_typed<D, false, true>(a, p, pipelined, s);
+  else
+    launch_typed<D, false, false>(a, p, pipelined, s);
 }
 
 }  // namespace
@@ -400,6 +586,8 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   const int64_t qb = (seq_len + kBlock - 1) / kBlock;
   DFS_REQUIRE(heads * qb < (int64_t(1) << 31) && qb * kBlock * head_dim < (int64_t(1) << 31),
               "%s: problem too large for 32-bit indexing", name);
+  // LDS: 128 KB of tiles (pipelined schedule) plus the row's column list.
+  DFS_REQUIRE(qb <= 8192, "%s: %lld key blocks exceed the LDS column list", name, (long long)qb);
   DFS_REQUIRE(scale > 0.f && isfinite(scale), "%s: scale must be positive and finite", name);
   BsaArgs a{static_cast<const uint16_t*>(q_perm), static_cast<const uint16_t*>(k_perm),
             static_cast<const uint16_t*>(v_t), row_ptr, col_idx, out, out_perm, lse};
@@ -413,11 +601,15 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   p.out_kind = out_dtype;
   const char* sched = getenv("DFSATTN_AMD_BSA_SCHED");
   p.sched = (sched && sched[0] == '1') ? 1 : 0;
+  const char* rot = getenv("DFSATTN_AMD_BSA_ROTATE");
+  p.rotate = (rot && rot[0] == '0') ? 0 : 1;
+  const char* kern = getenv("DFSATTN_AMD_BSA_KERNEL");
+  const bool pipelined = kern && kern[0] == 'p';  // "pipe" selects the one-workgroup pipelined schedule
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool qk_f16 = dtype == DFS_DTYPE_F16, pv_f16 = pv_dtype == DFS_DTYPE_F16;
   if (head_dim == 128)
-    launch_bsa<128>(a, p, qk_f16, pv_f16, s);
+    launch_bsa<128>(a, p, qk_f16, pv_f16, pipelined, s);
   else
-    launch_bsa<64>(a, p, qk_f16, pv_f16, s);
+    launch_bsa<64>(a, p, qk_f16, pv_f16, pipelined, s);
   return check_launch(name);
 }
