@@ -9,7 +9,13 @@ the fused inverse permutation.
 
 Prints one JSON line (metric = ms per call, lower is better) with the
 roofline of the attention kernel, per-phase kernel times and a CPU baseline
-(the fp32 oracle on a bounded sample of the same workload, scaled up).
+(the fp32 oracle on a bounded sample of the same inputs, scaled up).
+
+``--copy-calibration`` instead runs one plain 1 GiB device copy (torch's copy
+kernel), the known-size reference the FETCH_SIZE / WRITE_SIZE counters of the
+attention kernel are scaled by. The per-launch HBM traffic those counter runs
+give is kept in profiles/bsa_fwd_cfg1_traffic.txt and reported as
+``roofline.traffic``.
 """
 from __future__ import annotations
 
@@ -29,6 +35,7 @@ if ROOT not in sys.path:
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/f16 MFMA
 PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "bsa_fwd_cfg1_traffic.txt")
 
 
 def log(msg: str) -> None:
@@ -120,47 +127,73 @@ def run_gpu(args):
         "score_pooled_gflop": score_flop / 1e9,
         "density": flops / (4.0 * D * L * L * cfg.heads),
         "out_shape": list(out.shape),
+        "inputs": (q, k, v),
     }
 
 
-def cpu_baseline(time_budget_s: float = 20.0):
-    """fp32 oracle on the host cores on a bounded sample of the cfg-1 call:
-    scoring + top-k for 8 of 40 heads and masked attention for 96 query
-    blocks of 1 head, scaled linearly to the full call."""
+def cpu_baseline(q, k, v):
+    """fp32 oracle on the host cores, on the GPU run's own inputs (bf16 values
+    in fp32): Hilbert permutation + pooled scoring + top-k of all 40 heads, and
+    masked attention of every query block of 4 of the 40 heads (scaled x10).
+    About 15 s of CPU work on a 16-core host."""
     from oracle import dfs_oracle as orc
-    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+    from dfsattn_amd.workloads import CONFIGS
 
     cfg = CONFIGS[1]
-    sample_heads = 8
-    sub = type(cfg)(cfg.name, cfg.grid, sample_heads, cfg.head_dim, torch.float32, seed=cfg.seed)
-    log(f"cpu baseline: generating {sample_heads} heads on the host")
-    q, k, v = synth_qkv(sub, device="cpu", dtype=torch.float32)
+    att_heads = [0, 10, 20, 30]
+    log("cpu baseline: copying the inputs to the host")
+    q, k, v = (x.float().cpu() for x in (q, k, v))
     perm = torch.from_numpy(orc.hilbert3d_perm(*cfg.grid))
-    log("cpu baseline: scoring")
+    log("cpu baseline: permute + scoring + top-k (40 heads)")
     t0 = time.perf_counter()
     qp, kp, vp = (orc.apply_permutation(x, perm) for x in (q, k, v))
-    scores = orc.block_scores(qp, kp, cfg.tile, cfg.block, None, head_chunk=1)
+    scores = orc.block_scores(qp, kp, cfg.tile, cfg.block, None, head_chunk=4)
     mask = orc.mask_from_scores_wan(scores, cfg.sparsity)
     t_score = time.perf_counter() - t0
-    log(f"cpu baseline: scoring took {t_score:.1f} s; attention sample")
-    qblocks = list(range(0, 591, 6))[:96]
-    t1 = time.perf_counter()
-    orc.masked_attention(qp, kp, vp, mask, cfg.block, heads=[0], q_blocks=qblocks)
-    t_att = time.perf_counter() - t1
+    log(f"cpu baseline: scoring took {t_score:.1f} s; masked attention of {len(att_heads)} heads")
     n_qb = math.ceil(cfg.seq_len / cfg.block)
-    full_s = t_score * cfg.heads / sample_heads + t_att * (cfg.heads * n_qb) / len(qblocks)
+    t1 = time.perf_counter()
+    orc.masked_attention(qp, kp, vp, mask, cfg.block, heads=att_heads)
+    t_att = time.perf_counter() - t1
+    log(f"cpu baseline: attention sample took {t_att:.1f} s")
+    scale = cfg.heads / len(att_heads)
+    full_s = t_score + t_att * scale
     return {
-        "value": full_s * 1e3,
+        "value": round(full_s * 1e3, 1),
         "unit": "ms/call",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"cfg1 fp32 oracle: permute+scoring+top-k of {sample_heads}/40 heads "
-                   f"({t_score:.1f} s, x{cfg.heads // sample_heads}) + masked attention of "
-                   f"{len(qblocks)}/{n_qb} query blocks of 1 head ({t_att:.1f} s, "
-                   f"x{cfg.heads * n_qb / len(qblocks):.0f})"),
+        "sample": (f"cfg1 fp32 oracle on the benchmark inputs: permute+scoring+top-k of all 40 heads "
+                   f"({t_score:.1f} s) + masked attention of all {n_qb} query blocks of "
+                   f"{len(att_heads)}/40 heads ({t_att:.1f} s, x{scale:.0f}); unpermute not timed"),
         "host": {"os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
                  "torch_threads": torch.get_num_threads(), "cpu_model": _cpu_model()},
     }
+
+
+def read_traffic():
+    """Per-launch HBM bytes of the attention kernel at cfg1 from the committed
+    counter summary (``traffic_bytes_per_launch: N``), or None."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def copy_calibration():
+    """One 1 GiB device-to-device copy (after an untimed fill), for scaling
+    the FETCH_SIZE / WRITE_SIZE counters: the copy kernel's dispatch reads
+    and writes exactly 2**30 bytes."""
+    n = 1 << 28
+    src = torch.empty(n, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n * 4}), flush=True)
 
 
 def _cpu_model():
@@ -179,13 +212,19 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the DFS hot path is benchmarked on a single MI355X "
               "(multi-GPU sharding by head is a design note, not part of this build).", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     res = run_gpu(args)
-    cpu = None if args.no_cpu_baseline else cpu_baseline()
+    inputs = res.pop("inputs")
+    cpu = None if args.no_cpu_baseline else cpu_baseline(*inputs)
+    del inputs
     att_ms = res["phase_ms"]["attention"]
     line = {
         "metric": "DFS attn ms/call @75.6k tok,40h,d128 bf16; % bf16 MFMA peak on kept blocks",
@@ -205,8 +244,8 @@ def main():
                    "global_batch": 1, "seq_len": 75600, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(res["attention_tflops"], 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(res["attention_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "bsa_fwd_kernel", "kernel_ms": round(att_ms, 3),
+                     "frac": round(res["attention_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic(),
+                     "kernel": "bsa_fwd_split_kernel", "kernel_ms": round(att_ms, 3),
                      "algorithmic_flop": res["attention_flop"]},
         "phases_ms": {k_: round(v_, 3) for k_, v_ in res["phase_ms"].items()},
         "prepare_gbs": round(res["prepare_gbs"], 1),
