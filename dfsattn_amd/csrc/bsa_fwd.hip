@@ -2,33 +2,34 @@
 // block_sparse_attn_func called at dfsattn/attention_wan.py:379-386 and
 // dfsattn/attention_hyvideo.py:1075-1082).
 //
-// One workgroup = one (head, 128-row query block); four waves own 32 query
-// rows each and walk the CSR list of kept 128-key blocks. K (row-major) and
-// V^T (transposed by the permute kernel) tiles are copied straight from
-// global memory into LDS with 16-byte buffer loads.
-//
 // Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16 (lane column =
 // query, registers = keys), so the online-softmax row statistics need one
 // exchange between the two lane halves only. P is rounded to f16 (or bf16)
 // and multiplied with V^T as O^T += V^T P^T; the register order of the S^T
 // accumulator is reused as the token order of the PV operand, which the V^T
-// layout matches.
+// layout matches. K (row-major) and V^T (transposed by the permute kernel)
+// tiles are copied straight from global memory into LDS with 16-byte buffer
+// loads.
 //
 // Two schedules:
-//  * pipelined: one workgroup per CU, 512 registers per wave, K and
-//    V double-buffered in LDS (128 KB). Iteration i computes QK^T of block
-//    i+1 next to the softmax of block i, then P V of block i; one barrier per
-//    block, and the copies of the next blocks overlap a whole iteration.
-//  * split (default): two workgroups per CU, single K and V buffers, four
-//    barriers per block; the other workgroup on the CU fills the gaps.
+//  * split (default): one workgroup = one (head, 128-row query block), four
+//    waves of 32 query rows walking the row's kept key blocks; two
+//    workgroups per CU, single K and V buffers, the K copy of the next block
+//    overlapping softmax and PV, the V copy overlapping the next QK^T; the
+//    other workgroup on the CU fills the gaps.
+//  * duo (DFSATTN_AMD_BSA_KERNEL=duo): one eight-wave workgroup per CU for
+//    two adjacent query blocks, key blocks kept by both copied once (the
+//    schedule is described at the kernel).
 //
 // LDS rows are 256 bytes; 16-byte chunk c of row r is stored at chunk
 // c ^ (r % 16) so the 32 rows read by one MFMA operand fetch hit distinct
 // banks.
 #include <math.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "common.h"
+
 
 namespace dfs {
 namespace {
@@ -80,12 +81,12 @@ __device__ __forceinline__ void load_lds16(sgpr4 rs, uint32_t lds, uint32_t voff
                : "v"(voff), "s"(rs), "s"(soff), "{m0}"(lds));
 }
 
-// Copy of one tile into LDS with the chunk swizzle, all 256 threads taking
-// part: load j of wave w fills LDS bytes [(4j + w) * 1024, +1024), i.e. 1024/ROWB
-// rows. The swizzle depends on the row modulo the chunks per row, which is the
-// same for every j, so one per-thread byte offset serves all loads and the j-th
-// load only adds j * 4096 to the scalar offset.
-template <int ROWB>
+// Copy of one tile into LDS with the chunk swizzle by NW waves: load j of wave
+// w fills LDS bytes [(NW*j + w) * 1024, +1024), i.e. 1024/ROWB rows. The
+// swizzle depends on the row modulo the chunks per row, which is the same for
+// every j, so one per-thread byte offset serves all loads and the j-th load
+// only adds j * NW KiB to the scalar offset.
+template <int ROWB, int NW = 4>
 struct TileCopy {
   static constexpr int CPR = ROWB / 16;   // 16-byte chunks per row
   static constexpr int RPI = 64 / CPR;    // rows per wave instruction
@@ -94,7 +95,7 @@ struct TileCopy {
     const int r = wave * RPI + lane / CPR;
     voff = static_cast<uint32_t>(r * ROWB + (((lane % CPR) ^ (r % CPR)) * 16));
   }
-  // LOADS 16-byte loads per thread (4 * LOADS KiB in all) from byte tile_off.
+  // LOADS 16-byte loads per thread (NW * LOADS KiB in all) from byte tile_off.
   template <int LOADS>
   __device__ __forceinline__ void issue(sgpr4 rs, uint32_t tile_off, uint32_t lds_base,
                                         int wave) const {
@@ -103,7 +104,7 @@ struct TileCopy {
     asm volatile("" : "+s"(lds_base));
 #pragma unroll
     for (int j = 0; j < LOADS; ++j)
-      load_lds16(rs, lds_base + (j * 4 + wave) * 1024, voff, tile_off + j * 4096);
+      load_lds16(rs, lds_base + (j * NW + wave) * 1024, voff, tile_off + j * NW * 1024);
   }
 };
 
@@ -417,118 +418,373 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
   store_out<D>(p, out, out_perm, lse, o, m, lsum, h, qrow, hl);
 }
 
-template <int V>
-struct Parity {
-  static constexpr int value = V;
+// Helpers of the duo schedule below: key blocks streamed as 64-key halves.
+
+template <int G>
+__device__ __forceinline__ bool group_coords(const BsaParams& p, int& h, int& grp) {
+  const int groups = (p.Qb + G - 1) / G;
+  const int b = blockIdx.x, xcd = b & 7, i = b >> 3;
+  const int S = (groups + 7) >> 3;
+  h = i / S;
+  grp = xcd * S + (i - h * S);
+  return grp < groups;
+}
+
+// Copy of one V^T half block: D rows of 64 keys (128 bytes) taken from the
+// 256-byte rows of the V^T block, into LDS rows of 128 bytes. 16-byte chunk
+// c of row r is stored at chunk c ^ ((r >> 1) & 7): the 16 rows read by one
+// MFMA operand fetch then cover all 16 bank groups.
+struct VHalfCopy {
+  uint32_t voff;
+  __device__ __forceinline__ VHalfCopy(int wave, int lane) {
+    const int r = wave * 8 + (lane >> 3);  // 8 rows per wave instruction
+    voff = static_cast<uint32_t>(r * 256 + (((lane & 7) ^ ((r >> 1) & 7)) * 16));
+  }
+  // LOADS loads per thread (4 * LOADS KiB) of the half starting at byte off.
+  template <int LOADS>
+  __device__ __forceinline__ void issue(sgpr4 rs, uint32_t off, uint32_t lds_base, int wave) const {
+    asm volatile("" : "+s"(lds_base));
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j)  // load j of wave w: rows (4j + w) * 8 .. +7
+      load_lds16(rs, lds_base + (j * 4 + wave) * 1024, voff, off + j * 32 * 256);
+  }
 };
 
-// Pipelined schedule: one workgroup per CU (512 registers per wave), K and V
-// double-buffered. Block j lives in buffer j % 2. Iteration i: wait for the
-// copies issued one iteration earlier (K of block i+1, V of block i), barrier
-// (everybody finished iteration i-1, so K buffer i%2 and V buffer (i+1)%2 are
-// free), issue K of block i+2 and V of block i+1, then QK^T of block i+1
-// beside the softmax of block i, then P V of block i. Columns are ascending,
-// so only the last block can be the partial tail block; it is handled by the
-// peeled final iteration.
+__device__ __forceinline__ uint4 vhalf_chunk(const uint16_t* lds, int r, int c) {
+  return *reinterpret_cast<const uint4*>(lds + (r * 8 + (c ^ ((r >> 1) & 7))) * 8);
+}
+
+// The copies of the next stage (K half + V^T half of one key block, N loads
+// per thread), issued a few at a time between the MFMAs of the current stage
+// rather than in one burst: a burst of 1 KiB loads from every wave stalls the
+// waves at the load issue before they can compute. Part i goes out at the
+// (i * 6 / N)-th of the six issue points of a half step.
+template <int D>
+struct StageCopy {
+  static constexpr int K_LOADS = D / 32, V_LOADS = D / 32, N = K_LOADS + V_LOADS;
+  sgpr4 krs, vrs;
+  uint32_t kvoff, vvoff;
+  uint32_t koff, voff;  // global byte offsets of the pending stage
+  uint32_t kdst, vdst;  // LDS byte addresses of its buffers
+  int ws;
+  __device__ __forceinline__ void set(uint32_t col_off, int half, uint32_t dst) {
+    koff = col_off + half * (128 * D);  // 64 K rows of 2D bytes
+    voff = col_off + half * 128;        // 64 keys of each 256-byte V^T row
+    kdst = dst;
+    vdst = dst + 64 * D * 2;
+    asm volatile("" : "+s"(koff), "+s"(voff), "+s"(kdst), "+s"(vdst));
+  }
+  template <int I>
+  __device__ __forceinline__ void part() const {
+    if constexpr (I < K_LOADS)
+      load_lds16(krs, kdst + (I * 4 + ws) * 1024, kvoff, koff + I * 4 * 1024);
+    else
+      load_lds16(vrs, vdst + ((I - K_LOADS) * 4 + ws) * 1024, vvoff, voff + (I - K_LOADS) * 32 * 256);
+  }
+  template <int E, int I = 0>
+  __device__ __forceinline__ void at() const {
+    if constexpr (I < N) {
+      if constexpr (I * 6 / N == E) part<I>();
+      at<E, I + 1>();
+    }
+  }
+  template <int I = 0>
+  __device__ __forceinline__ void all() const {
+    if constexpr (I < N) {
+      part<I>();
+      all<I + 1>();
+    }
+  }
+};
+
+// Per-lane LDS byte addresses of the operand rows of one half step. The
+// swizzled 16-byte chunk of an operand read is (2 * step) ^ y for a lane
+// constant y, formed at the read with one XOR-add (v_xad_u32) instead of being
+// kept in registers for every step: the two-query-block kernel has none to
+// spare.
+struct HalfAddr {
+  uint32_t k_row;  // K half: byte address of row l32 (chunk 0)
+  uint32_t ky;     // (hl ^ (l32 & 15)) << 4
+  uint32_t v_row;  // V^T half: byte address of row l32 (chunk 0)
+  uint32_t vy;     // (hl ^ ((l32 >> 1) & 7)) << 4
+};
+
+template <int D>
+__device__ __forceinline__ HalfAddr half_addr(uint32_t k_half, uint32_t v_half, int l32, int hl) {
+  HalfAddr a;
+  a.k_row = k_half + static_cast<uint32_t>(l32 * D * 2);
+  a.ky = static_cast<uint32_t>((hl ^ (l32 & (D / 8 - 1))) << 4);
+  a.v_row = v_half + static_cast<uint32_t>(l32 * 128);
+  a.vy = static_cast<uint32_t>((hl ^ ((l32 >> 1) & 7)) << 4);
+  return a;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(3))) u32x4* lds_u32x4_ptr;
+
+// 16-byte LDS read at byte address addr.
+__device__ __forceinline__ uint4 lds_read16(uint32_t addr) {
+  const u32x4 v = *(lds_u32x4_ptr)(static_cast<uintptr_t>(addr));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// One 64-key half step for one query block: S^T in 32-key chunks of online
+// softmax (NC chunks per pass), then O^T += V^T P^T.
+template <int D, typename QkOp, typename PvOp, int NC, typename CP>
+__device__ __forceinline__ void half_step(HalfAddr ad, const typename QkOp::vec* qf, float scale_log2, float& m,
+                                          float& lsum, f32x16* o, int valid, int hl, const CP& cp) {
+  constexpr int DS = D / 16, DCH = D / 32;
+  // Fresh each step: keeps the per-step addresses out of the loop-carried
+  // register set.
+  asm volatile("" : "+v"(ad.k_row), "+v"(ad.ky), "+v"(ad.v_row), "+v"(ad.vy));
+#pragma unroll
+  for (int c0 = 0; c0 < 2; c0 += NC) {
+    f32x16 s[NC];
+#pragma unroll
+    for (int kc = 0; kc < NC; ++kc) {
+      s[kc] = f32x16{};
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const uint4 a = lds_read16((((2u * ds) << 4) ^ ad.ky) + ad.k_row + (c0 + kc) * 32 * D * 2);
+        s[kc] = QkOp::run(__builtin_bit_cast(typename QkOp::vec, a), qf[ds], s[kc]);
+      }
+      // Issue points: QK chunk ends, then PV step ends, in program order.
+      if constexpr (NC == 2) {
+        if (kc == 0) cp.template at<0>(); else cp.template at<1>();
+      } else {
+        if (c0 == 0) cp.template at<0>(); else cp.template at<3>();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (valid < 64) {  // keys >= valid of this half are past L
+#pragma unroll
+      for (int kc = 0; kc < NC; ++kc)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if ((c0 + kc) * 32 + (r >> 2) * 8 + hl * 4 + (r & 3) >= valid) s[kc][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kc = 0; kc < NC; ++kc)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kc][r]);
+    const float mnew = fmaxf(m, xhalf_max(mx) * scale_log2);
+    if (__any(mnew > m)) {
+      const float alpha = exp2_fast(m - mnew);  // 0 for an empty state (m = -inf, mnew finite)
+      lsum *= alpha;
+#pragma unroll
+      for (int i = 0; i < DCH; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+    }
+    m = mnew;
+    // A fully masked chunk seen before any key: exponentiate against 0 so
+    // P = exp2(-inf) = 0, not NaN.
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+#pragma unroll
+    for (int ks = 0; ks < 2 * NC; ++ks) {
+      const f32x16& src = s[ks >> 1];
+      const int r0 = (ks & 1) * 8;
+      typename PvOp::pair pr[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pr[j] = PvOp::pack(exp2_fast(fmaf(src[r0 + 2 * j], scale_log2, -mref)),
+                           exp2_fast(fmaf(src[r0 + 2 * j + 1], scale_log2, -mref)));
+        lsum = PvOp::sum2(pr[j], lsum);
+      }
+      const typename PvOp::vec pf = __builtin_bit_cast(typename PvOp::vec, pr);
+      const uint32_t vcol = ((2u * (c0 * 2 + ks)) << 4) ^ ad.vy;
+#pragma unroll
+      for (int dc = 0; dc < DCH; ++dc) {
+        const uint4 a = lds_read16(vcol + ad.v_row + dc * 32 * 128);
+        o[dc] = PvOp::run(__builtin_bit_cast(typename PvOp::vec, a), pf, o[dc]);
+      }
+      if constexpr (NC == 2) {
+        if (ks == 0) cp.template at<2>();
+        else if (ks == 1) cp.template at<3>();
+        else if (ks == 2) cp.template at<4>();
+        else cp.template at<5>();
+      } else {
+        if (c0 == 0) { if (ks == 0) cp.template at<1>(); else cp.template at<2>(); }
+        else { if (ks == 0) cp.template at<4>(); else cp.template at<5>(); }
+      }
+    }
+  }
+}
+
+// Duo schedule: one workgroup of eight waves per CU serves two adjacent query
+// blocks A and B; waves 0-3 own A's 32-row groups, waves 4-7 B's. The
+// columns kept by both are shared slots (one key block, read by both
+// groups); the columns kept by only one of them are paired up, one of A's
+// with one of B's, into slots carrying two key blocks. Every wave works in
+// every slot (except the few unpaired ones), each on one query block, so the
+// per-wave registers stay those of a single query block while the bytes
+// copied are those of the union of the two rows. Slots are streamed as
+// 64-key halves through double buffers; a stage holds region A (K and V^T
+// halves of A's block) and region B (B's block, unused for shared slots).
 template <int D, bool QK_F16, bool PV_F16>
-__global__ void __launch_bounds__(256, 1) bsa_fwd_pipe_kernel(BSA_KERNEL_ARGS) {
-  constexpr int DCH = D / 32;
-  constexpr int K_LOADS = D / 16;
-  constexpr int V_LOADS = D / 16;
+__global__ void __launch_bounds__(512, 1) bsa_fwd_duo_kernel(BSA_KERNEL_ARGS) {
   constexpr uint32_t TILE_BYTES = 128 * D * 2;
-  constexpr int TILE = 128 * D;  // uint16 elements per tile
+  constexpr int HALF = 64 * D;                   // uint16 elements of a K (or V^T) half
+  constexpr int REGION = 2 * HALF;               // K half + V^T half
+  constexpr int STAGE = 2 * REGION;              // regions A and B
+  constexpr uint16_t NONE = 0xFFFF;
   typedef MfmaOp<QK_F16> QkOp;
   typedef MfmaOp<PV_F16> PvOp;
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2 * TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2 * TILE];
-  extern __shared__ int32_t cols[];
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[2 * STAGE];
+  __shared__ int n_slots;
+  // Dynamic LDS: bitmaps of A and B (W words each), then the slot columns
+  // col_a[Kb], col_b[Kb] (uint16, NONE when the slot has no block there).
+  extern __shared__ uint32_t dyn[];
 
-  int h, qb;
-  if (!wg_coords(p, h, qb)) return;
+  int h, grp;
+  if (!group_coords<2>(p, h, grp)) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int64_t row = static_cast<int64_t>(h) * p.Qb + qb;
-  const int beg = row_ptr[row];
-  const int n = min(max(row_ptr[row + 1] - beg, 0), p.Kb);
-  const int qrow = qb * 128 + w * 32 + l32;
+  const int g = __builtin_amdgcn_readfirstlane(w >> 2), rg = w & 3;  // wave-uniform
+  const int W = (p.Kb + 31) >> 5;
+  uint32_t* bm = dyn;  // [2][W]
+  uint16_t* col_a = reinterpret_cast<uint16_t*>(dyn + 2 * W);
+  uint16_t* col_b = col_a + p.Kb;
 
+  for (int i = tid; i < 2 * W; i += 512) bm[i] = 0u;
+  for (int i = tid; i < 2 * p.Kb; i += 512) col_a[i] = NONE;
+  block_barrier();
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int qr = grp * 2 + r;
+    if (qr < p.Qb) {
+      const int64_t row = static_cast<int64_t>(h) * p.Qb + qr;
+      const int beg = row_ptr[row];
+      const int n = min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
+      for (int i = tid; i < n; i += 512) {
+        const int c = col_idx[beg + i];
+        if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb))
+          atomicOr(&bm[r * W + (c >> 5)], 1u << (c & 31));
+      }
+    }
+  }
+  block_barrier();
+  if (w == 0) {
+    // Shared columns fill slots 0.. in ascending order; A-only columns fill
+    // col_a and B-only columns col_b of the slots after them, each ascending.
+    const int per = (W + 63) >> 6;  // words per lane
+    const int w0 = lane * per;
+    int cs = 0, ca = 0, cb = 0;
+    for (int j = 0; j < per && w0 + j < W; ++j) {
+      const uint32_t a = bm[w0 + j], b = bm[W + w0 + j];
+      cs += __popc(a & b);
+      ca += __popc(a & ~b);
+      cb += __popc(b & ~a);
+    }
+    int is = cs, ia = ca, ib = cb;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int ys = __shfl_up(is, off, 64), ya = __shfl_up(ia, off, 64), yb = __shfl_up(ib, off, 64);
+      if (lane >= off) {
+        is += ys;
+        ia += ya;
+        ib += yb;
+      }
+    }
+    const int n_shared = __shfl(is, 63, 64);
+    int ps = is - cs, pa = n_shared + ia - ca, pb = n_shared + ib - cb;
+    for (int j = 0; j < per && w0 + j < W; ++j) {
+      const uint32_t a = bm[w0 + j], b = bm[W + w0 + j];
+      uint32_t x = a & b;
+      while (x) {
+        const int c = (w0 + j) * 32 + __ffs(x) - 1;
+        x &= x - 1;
+        col_a[ps] = static_cast<uint16_t>(c);
+        col_b[ps] = static_cast<uint16_t>(c);
+        ++ps;
+      }
+      x = a & ~b;
+      while (x) {
+        col_a[pa++] = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
+        x &= x - 1;
+      }
+      x = b & ~a;
+      while (x) {
+        col_b[pb++] = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
+        x &= x - 1;
+      }
+    }
+    if (lane == 63) n_slots = n_shared + max(ia, ib);
+  }
+
+  constexpr int DCH = D / 32;
   f32x16 o[DCH];
 #pragma unroll
   for (int i = 0; i < DCH; ++i) o[i] = f32x16{};
   float m = -INFINITY, lsum = 0.f;
+  typename QkOp::vec qf[D / 16];
+  const int qb = grp * 2 + g;
+  const int qrow = qb * 128 + rg * 32 + l32;
+  if (qb < p.Qb) {
+    load_q<D, QkOp>(q, p, h, qrow, hl, qf);
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qf[s]));
+  }
+  block_barrier();
+  const int T = __builtin_amdgcn_readfirstlane(n_slots);
 
-  if (n > 0) {
+  if (T > 0) {
     const uint32_t head_bytes = static_cast<uint32_t>(p.R) * D * 2;
     const sgpr4 krs = make_rsrc(k + static_cast<int64_t>(h) * p.R * D, head_bytes);
     const sgpr4 vrs = make_rsrc(vt + static_cast<int64_t>(h) * p.R * D, head_bytes);
-    const uint32_t k_base = lds_addr(k_lds), v_base = lds_addr(v_lds);
-    const int ws = __builtin_amdgcn_readfirstlane(w);
-    const TileCopy<D * 2> kcopy(ws, lane);
-    const TileCopy<256> vcopy(ws, lane);
-    typename QkOp::vec qf[D / 16];
-    load_q<D, QkOp>(q, p, h, qrow, hl, qf);
-    for (int i = tid; i < n; i += 256) cols[i] = col_idx[beg + i];
-#pragma unroll
-    for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qf[s]));
-    block_barrier();
-    // Column of block j, or the out-of-range sentinel Kb past the end (its
-    // copies fetch nothing), so every iteration issues the same loads.
-    auto col = [&](int j) -> int {
-      const int c = __builtin_amdgcn_readfirstlane(cols[min(j, n - 1)]);
-      return j < n ? c : p.Kb;
+    const uint32_t base = lds_addr(tiles);
+    const int ws = __builtin_amdgcn_readfirstlane(rg);  // wave index within its group
+    StageCopy<D> cp;
+    cp.krs = krs;
+    cp.vrs = vrs;
+    cp.kvoff = TileCopy<D * 2>(ws, lane).voff;
+    cp.vvoff = VHalfCopy(ws, lane).voff;
+    cp.ws = ws;
+    const bool tail_possible = (p.L & 127) != 0;
+    // Group 0 copies slot blocks into region A, group 1 into region B; a
+    // region with nothing to hold copies the out-of-range block Kb (zeros,
+    // nothing fetched) so every wave issues the same loads every stage.
+    auto copy_col = [&](int t) -> int {
+      if (t >= T) return p.Kb;
+      const int a = __builtin_amdgcn_readfirstlane(static_cast<int>(col_a[t]));
+      if (g == 0) return a == NONE ? p.Kb : a;
+      const int b = __builtin_amdgcn_readfirstlane(static_cast<int>(col_b[t]));
+      return (b == NONE || b == a) ? p.Kb : b;
     };
-
-    // Prologue: K of blocks 0 and 1, V of block 0; QK^T of block 0.
-    kcopy.template issue<K_LOADS>(krs, col(0) * TILE_BYTES, k_base, ws);
-    kcopy.template issue<K_LOADS>(krs, col(1) * TILE_BYTES, k_base + TILE_BYTES, ws);
-    vcopy.template issue<V_LOADS>(vrs, col(0) * TILE_BYTES, v_base, ws);
-    wait_vmcnt_0();
-    block_barrier();
-    f32x16 sa[4], sb[4];
-    qk_tile<D, QkOp>(k_lds, qf, l32, hl, sa);
-
-    // One steady-state iteration with compile-time buffer parity PAR (= i % 2).
-    auto step = [&](int i, f32x16* s_cur, f32x16* s_next, auto par_tag) {
-      constexpr int PAR = decltype(par_tag)::value;
-      wait_vmcnt_0();  // K of block i+1, V of block i
-      block_barrier();
-      kcopy.template issue<K_LOADS>(krs, col(i + 2) * TILE_BYTES, k_base + PAR * TILE_BYTES, ws);
-      vcopy.template issue<V_LOADS>(vrs, col(i + 1) * TILE_BYTES, v_base + (1 - PAR) * TILE_BYTES, ws);
-      qk_tile<D, QkOp>(k_lds + (1 - PAR) * TILE, qf, l32, hl, s_next);
-      const float mnew = softmax_max<DCH, false>(s_cur, p.scale_log2, m, lsum, o);
-      pv_tile<D, PvOp>(v_lds + PAR * TILE, s_cur, p.scale_log2, mnew, lsum, o, l32, hl);
-      // Interleave: LDS operand reads run ahead, every MFMA is followed by the
-      // next read and a few VALU instructions (softmax of this block).
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    auto stage_dst = [&](int half) { return base + static_cast<uint32_t>((half * STAGE + g * REGION) * 2); };
+    int cc = copy_col(0);
+    cp.set(static_cast<uint32_t>(cc) * TILE_BYTES, 0, stage_dst(0));
+    cp.all();
+    for (int t = 0; t < T; ++t) {
+      const int cn = copy_col(t + 1);
+      const int a = __builtin_amdgcn_readfirstlane(static_cast<int>(col_a[t]));
+      const int b = __builtin_amdgcn_readfirstlane(static_cast<int>(col_b[t]));
+      const int mine = g == 0 ? a : b;                 // this group's block in slot t
+      const int reg = (g == 1 && b != a) ? 1 : 0;      // region holding it
+      int valid = 128;
+      if (tail_possible && mine == p.Kb - 1) valid = p.L - mine * 128;
 #pragma unroll
-      for (int g = 0; g < 64; ++g) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      for (int half = 0; half < 2; ++half) {
+        wait_vmcnt_0();   // this wave's copies of this stage have landed
+        block_barrier();  // everybody's, and the previous stage is no longer read
+        // The next stage: the other half of this slot, or half 0 of the next.
+        if (half == 0)
+          cp.set(static_cast<uint32_t>(cc) * TILE_BYTES, 1, stage_dst(1));
+        else
+          cp.set(static_cast<uint32_t>(cn) * TILE_BYTES, 0, stage_dst(0));
+        if (mine != NONE) {
+          const uint32_t rb = base + static_cast<uint32_t>((half * STAGE + reg * REGION) * 2);
+          const HalfAddr ad = half_addr<D>(rb, rb + HALF * 2, l32, hl);
+          half_step<D, QkOp, PvOp, 2>(ad, qf, p.scale_log2, m, lsum, o, valid - half * 64, hl, cp);
+        } else {
+          cp.all();
+        }
       }
-    };
-    int i = 0;
-    for (; i + 2 < n; i += 2) {
-      step(i, sa, sb, Parity<0>{});
-      step(i + 1, sb, sa, Parity<1>{});
+      cc = cn;
     }
-    // One or two blocks remain; the last one may be the partial tail block.
-    auto last = [&](int j, f32x16* s_cur, auto par_tag) {
-      constexpr int PAR = decltype(par_tag)::value;
-      wait_vmcnt_0();  // V of block j
-      block_barrier();
-      const int kb = col(j);
-      if ((p.L & 127) != 0 && kb == p.Kb - 1) mask_tail(s_cur, p.L - kb * 128, hl);
-      const float mnew = softmax_max<DCH, false>(s_cur, p.scale_log2, m, lsum, o);
-      pv_tile<D, PvOp>(v_lds + PAR * TILE, s_cur, p.scale_log2, mnew, lsum, o, l32, hl);
-    };
-    if (i + 1 < n) {
-      step(i, sa, sb, Parity<0>{});
-      last(i + 1, sb, Parity<1>{});
-    } else {
-      last(i, sa, Parity<0>{});
-    }
+    wait_vmcnt_0();  // the trailing (empty) copies have retired
   }
-  store_out<D>(p, out, out_perm, lse, o, m, lsum, h, qrow, hl);
+  if (qb < p.Qb) store_out<D>(p, out, out_perm, lse, o, m, lsum, h, qrow, hl);
 }
 
 struct BsaArgs {
@@ -539,27 +795,37 @@ struct BsaArgs {
   float* lse;
 };
 
+enum BsaSchedule { kSplit = 0, kDuo = 1 };
+
 template <int D, bool QK_F16, bool PV_F16>
-void launch_typed(const BsaArgs& a, const BsaParams& p, bool pipelined, hipStream_t s) {
+void launch_duo(const BsaArgs& a, const BsaParams& p, hipStream_t s) {
+  const int groups = (p.Qb + 1) / 2, S = (groups + 7) / 8;
+  const int W = (p.Kb + 31) / 32;
+  const size_t smem = static_cast<size_t>(2 * W) * sizeof(uint32_t) + static_cast<size_t>(p.Kb) * 4;
+  bsa_fwd_duo_kernel<D, QK_F16, PV_F16><<<dim3(static_cast<unsigned>(8 * S * p.H)), 512, smem, s>>>(
+      a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out, a.out_perm, a.lse, p);
+}
+
+template <int D, bool QK_F16, bool PV_F16>
+void launch_typed(const BsaArgs& a, const BsaParams& p, BsaSchedule sched, hipStream_t s) {
+  // The duo schedule keeps two slot column lists in LDS beside 128 KB of
+  // tiles; beyond 4096 key blocks the split schedule runs instead.
+  if (sched == kDuo && p.Kb <= 4096) return launch_duo<D, QK_F16, PV_F16>(a, p, s);
   const int S = (p.Qb + 7) / 8;
   dim3 grid(static_cast<unsigned>(p.sched == 0 ? 8 * S * p.H : p.H * p.Qb));
   const size_t smem = static_cast<size_t>(p.Kb) * sizeof(int32_t);
-  if (pipelined)
-    bsa_fwd_pipe_kernel<D, QK_F16, PV_F16><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
-                                                                  a.out_perm, a.lse, p);
-  else
-    bsa_fwd_split_kernel<D, QK_F16, PV_F16><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
-                                                                   a.out_perm, a.lse, p);
+  bsa_fwd_split_kernel<D, QK_F16, PV_F16><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
+                                                                 a.out_perm, a.lse, p);
 }
 
 template <int D>
-void launch_bsa(const BsaArgs& a, const BsaParams& p, bool qk_f16, bool pv_f16, bool pipelined, hipStream_t s) {
+void launch_bsa(const BsaArgs& a, const BsaParams& p, bool qk_f16, bool pv_f16, BsaSchedule sched, hipStream_t s) {
   if (qk_f16)
-    launch_typed<D, true, true>(a, p, pipelined, s);
+    launch_typed<D, true, true>(a, p, sched, s);
   else if (pv_f16)
-    launch_typed<D, false, true>(a, p, pipelined, s);
+    launch_typed<D, false, true>(a, p, sched, s);
   else
-    launch_typed<D, false, false>(a, p, pipelined, s);
+    launch_typed<D, false, false>(a, p, sched, s);
 }
 
 }  // namespace
@@ -586,7 +852,7 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   const int64_t qb = (seq_len + kBlock - 1) / kBlock;
   DFS_REQUIRE(heads * qb < (int64_t(1) << 31) && qb * kBlock * head_dim < (int64_t(1) << 31),
               "%s: problem too large for 32-bit indexing", name);
-  // LDS: 128 KB of tiles (pipelined schedule) plus the row's column list.
+  // LDS: 64 KB of tiles (split schedule) plus the row's column list.
   DFS_REQUIRE(qb <= 8192, "%s: %lld key blocks exceed the LDS column list", name, (long long)qb);
   DFS_REQUIRE(scale > 0.f && isfinite(scale), "%s: scale must be positive and finite", name);
   BsaArgs a{static_cast<const uint16_t*>(q_perm), static_cast<const uint16_t*>(k_perm),
@@ -599,17 +865,18 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   p.Kb = static_cast<int>(qb);
   p.scale_log2 = scale * 1.4426950408889634f;
   p.out_kind = out_dtype;
-  const char* sched = getenv("DFSATTN_AMD_BSA_SCHED");
-  p.sched = (sched && sched[0] == '1') ? 1 : 0;
+  const char* order = getenv("DFSATTN_AMD_BSA_SCHED");
+  p.sched = (order && order[0] == '1') ? 1 : 0;
   const char* rot = getenv("DFSATTN_AMD_BSA_ROTATE");
   p.rotate = (rot && rot[0] == '0') ? 0 : 1;
+  // DFSATTN_AMD_BSA_KERNEL: "split" (default) or "duo".
   const char* kern = getenv("DFSATTN_AMD_BSA_KERNEL");
-  const bool pipelined = kern && kern[0] == 'p';  // "pipe" selects the one-workgroup pipelined schedule
+  const BsaSchedule sched = (kern && strcmp(kern, "duo") == 0) ? kDuo : kSplit;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool qk_f16 = dtype == DFS_DTYPE_F16, pv_f16 = pv_dtype == DFS_DTYPE_F16;
   if (head_dim == 128)
-    launch_bsa<128>(a, p, qk_f16, pv_f16, pipelined, s);
+    launch_bsa<128>(a, p, qk_f16, pv_f16, sched, s);
   else
-    launch_bsa<64>(a, p, qk_f16, pv_f16, pipelined, s);
+    launch_bsa<64>(a, p, qk_f16, pv_f16, sched, s);
   return check_launch(name);
 }

@@ -181,11 +181,18 @@ def _run_bsa(dev, q, k, v, mask_bool, pv, out_dtype, perm=None):
     return out.cpu()
 
 
+SCHEDULES = ("split", "duo")
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
 @pytest.mark.parametrize("d,length,density,pv", [
     (128, 1000, 0.3, torch.float16), (128, 1024, 0.5, torch.float16), (64, 1000, 0.3, torch.float16),
     (128, 3000, 0.3, torch.float16), (128, 1000, 1.0, torch.float16), (128, 1000, 0.3, torch.bfloat16),
-    (64, 130, 1.0, torch.float16)])
-def test_bsa_fwd_matches_masked_dense(dev, d, length, density, pv):
+    (64, 130, 1.0, torch.float16), (128, 1100, 0.3, torch.float16), (64, 1400, 0.2, torch.bfloat16)])
+def test_bsa_fwd_matches_masked_dense(dev, monkeypatch, schedule, d, length, density, pv):
+    """Every attention schedule (DFSATTN_AMD_BSA_KERNEL) against fp32 masked
+    attention; odd block counts leave the last query-block pair half empty."""
+    monkeypatch.setenv("DFSATTN_AMD_BSA_KERNEL", schedule)
     from dfsattn_amd.workloads import DfsConfig, synth_qkv
     heads = 2
     cfg = DfsConfig("t", (1, 1, length), heads, d, torch.bfloat16, seed=11)
@@ -221,7 +228,9 @@ def test_bsa_fwd_bf16_out_and_fused_unpermute(dev):
     assert torch.equal(scat[:, :, perm], out32)
 
 
-def test_empty_rows_give_zero(dev):
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_empty_rows_give_zero(dev, monkeypatch, schedule):
+    monkeypatch.setenv("DFSATTN_AMD_BSA_KERNEL", schedule)
     heads, d, length = 1, 128, 512
     q, k, v = (torch.randn((1, heads, length, d)).to(torch.bfloat16) for _ in range(3))
     mask = torch.zeros((heads, 4, 4), dtype=torch.bool)
@@ -230,3 +239,26 @@ def test_empty_rows_give_zero(dev):
     assert torch.count_nonzero(out[:, :, 128:]) == 0
     ref = orc.masked_attention(q, k, v, mask)
     assert mean_rel(out[:, :, :128], ref[:, :, :128]) < 1e-3
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_rows_keeping_only_a_short_tail_block(dev, monkeypatch, schedule):
+    """The last block holds 26 keys: a wave whose keys of that block are all
+    masked, and which has seen no other key, must contribute nothing."""
+    monkeypatch.setenv("DFSATTN_AMD_BSA_KERNEL", schedule)
+    heads, d, length = 2, 128, 1050
+    q, k, v = (torch.randn((1, heads, length, d), generator=torch.Generator().manual_seed(s)).to(torch.bfloat16)
+               for s in (21, 22, 23))
+    nb = math.ceil(length / 128)
+    mask = torch.rand((heads, nb, nb), generator=torch.Generator().manual_seed(24)) < 0.3
+    mask[:, 0] = False
+    mask[:, 0, nb - 1] = True   # only the tail block
+    mask[:, 1] = False
+    mask[:, 1, 3] = True
+    mask[:, 1, nb - 1] = True
+    mask[:, nb - 1] = False
+    mask[:, nb - 1, nb - 1] = True
+    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32)
+    assert torch.isfinite(out).all()
+    ref = orc.masked_attention(q, k, v, mask)
+    assert float((out - ref).abs().max()) <= 2e-2 and mean_rel(out, ref) <= 1e-3
