@@ -11,6 +11,13 @@ Prints one JSON line (metric = ms per call, lower is better) with the
 roofline of the attention kernel, per-phase kernel times and a CPU baseline
 (the fp32 oracle on a bounded sample of the same inputs, scaled up).
 
+``--workload cfg2`` measures the HunyuanVideo call instead (configs[2]:
+118,800 video + 256 text tokens, 24 heads), and ``--workload cfg3`` the
+mask-cache regime (configs[3]: 50 denoising calls at the cfg1 shape with
+Q, K drifting by N(0, 0.02) per step, 12 dense warm-up steps, a mask refresh
+every 12 steps, sparsity in {0.1, 0.2, 0.3, 0.5}, sparsity_dcrt 0 and 0.1);
+each prints its own JSON line. The default run (cfg1) is the benchmark line.
+
 ``--copy-calibration`` instead runs one plain 1 GiB device copy (torch's copy
 kernel), the known-size reference the FETCH_SIZE / WRITE_SIZE counters of the
 attention kernel are scaled by. The per-launch HBM traffic those counter runs
@@ -131,6 +138,122 @@ def run_gpu(args):
     }
 
 
+def run_cfg2(args):
+    """HunyuanVideo joint attention at configs[2], fresh mask every call."""
+    from dfsattn_amd.attention_hyvideo import DFS_Attention, _dfs_attention_instances, dfs_attention
+    from dfsattn_amd.layout import csr_flops
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[2]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("generating cfg2 inputs on the GPU")
+    q, k, v = synth_qkv(cfg, device=dev)
+    perm = hilbert3d_perm(*cfg.grid)
+
+    def step():
+        return dfs_attention(q, k, v, step_idx=12, skip_steps=12, cache_interval=12, layer_idx=0,
+                             sparsity=cfg.sparsity, sparsity_dcrt=0.0, tile_size=cfg.tile, block_size=cfg.block,
+                             video_len=cfg.video_len, video_perm=perm, cache_flag=True)
+
+    for i in range(args.warmup):
+        step()
+        torch.cuda.synchronize()
+        log(f"warmup step {i + 1}/{args.warmup} done")
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    entry = next(iter(DFS_Attention._cached_metadata.values()))
+    flops = csr_flops(entry["row_ptr"].cpu().numpy(), entry["col_idx"].cpu().numpy(), cfg.heads, cfg.seq_len,
+                      cfg.head_dim)
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()
+    log(f"cfg2: {ms:.3f} ms/call, {flops / ms / 1e9:.1f} effective TFLOP/s")
+    return {"metric": "DFS attn ms/call @119,056 tok (118,800 video + 256 text),24h,d128 bf16",
+            "value": round(ms, 3), "unit": "ms/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic (smoothed-field Q/K, iid V, iid text; seeded)",
+            "config": {"workload": "cfg2 HunyuanVideo joint attention: 33x45x80 video + 256 text tokens, 24 heads, "
+                                   "d128, tile 16, block 128, hilbert3d, sparsity 0.3, fresh mask per call",
+                       "global_batch": 1, "seq_len": cfg.seq_len, "parallelism": "none (1 GPU)"},
+            "effective_tflops": round(flops / ms / 1e9, 1), "kept_flop": flops,
+            "frac_of_bf16_peak": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
+
+
+def run_cfg3(args):
+    """Mask-cache regime over a sparsity sweep: 50 calls, the
+    first 12 dense (full attention on the same kernel), a mask refresh every
+    12 steps, Q and K drifting by N(0, 0.02) per step."""
+    from dfsattn_amd.attention_wan import DFS_Attention, _compute_cache_schedule, _dfs_attention_instances, dfs_attention
+    from dfsattn_amd.fullattention import full_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, drift, synth_qkv
+
+    cfg = CONFIGS[1]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("generating cfg1 inputs on the GPU")
+    q0, k0, v = synth_qkv(cfg, device=dev)
+    perm = hilbert3d_perm(*cfg.grid)
+    L = cfg.seq_len
+    cu = torch.tensor([0, L, L], dtype=torch.int32, device=dev)
+    steps, skip, interval = 50, 12, 12
+    runs = []
+    for dcrt in (0.0, 0.1):
+        for s in (0.1, 0.2, 0.3, 0.5):
+            DFS_Attention.clear_cache()
+            _dfs_attention_instances.clear()
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(1234)
+            q, k = q0.clone(), k0.clone()
+            evs = []
+            for t in range(steps):
+                if t:
+                    q, k = drift(q, 0.02, gen), drift(k, 0.02, gen)
+                a, b = _events()
+                a.record()
+                if t < skip:
+                    full_attention(q, k, v, mode="flash", cu_seqlens_q=cu, cu_seqlens_kv=cu, max_seqlen_q=L,
+                                   max_seqlen_kv=L)
+                else:
+                    dfs_attention(q, k, v, step_idx=2 * t, skip_steps=skip, cache_interval=interval, layer_idx=0,
+                                  sparsity=s, sparsity_dcrt=dcrt, tile_size=cfg.tile, block_size=cfg.block,
+                                  video_perm=perm, cache_flag=True)
+                b.record()
+                evs.append((a, b))
+            torch.cuda.synchronize()
+            ms = [a.elapsed_time(b) for a, b in evs]
+            refresh = [t for t in range(skip, steps)
+                       if _compute_cache_schedule(2 * t, 2 * skip, 2 * interval, s, dcrt)[0]]
+            cached = [t for t in range(skip, steps) if t not in refresh]
+            mean = lambda xs: float(np.mean(xs)) if xs else None  # noqa: E731
+            run = {"sparsity": s, "sparsity_dcrt": dcrt, "amortized_ms_per_step": round(mean(ms), 3),
+                   "dense_step_ms": round(mean(ms[:skip]), 3),
+                   "refresh_steps": refresh, "refresh_step_ms": round(mean([ms[t] for t in refresh]), 3),
+                   "cached_step_ms": round(mean([ms[t] for t in cached]), 3),
+                   "sparse_amortized_ms": round(mean(ms[skip:]), 3)}
+            run["mask_recompute_ms"] = round(run["refresh_step_ms"] - run["cached_step_ms"], 3)
+            log(f"cfg3 s={s} dcrt={dcrt}: {run}")
+            runs.append(run)
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()
+    base = next(r for r in runs if r["sparsity"] == 0.3 and r["sparsity_dcrt"] == 0.0)
+    return {"metric": "DFS mask-cache regime amortized ms/step @75.6k tok,40h,d128 bf16 (50 steps)",
+            "value": base["amortized_ms_per_step"], "unit": "ms/step", "n_gpus": 1, "steps": steps, "warmup": 0,
+            "ms_per_step": base["amortized_ms_per_step"], "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic cfg1 inputs, Q/K drift N(0,0.02) per step (seeded)",
+            "config": {"workload": "cfg3 mask-cache regime: 50 calls, skip_steps 12 (dense), cache_interval 12, "
+                                   "value = sparsity 0.3, sparsity_dcrt 0", "global_batch": 1, "seq_len": L,
+                       "parallelism": "none (1 GPU)"},
+            "sweep": runs}
+
+
 def cpu_baseline(q, k, v):
     """fp32 oracle on the host cores, on the GPU run's own inputs (bf16 values
     in fp32): Hilbert permutation + pooled scoring + top-k of all 40 heads, and
@@ -213,6 +336,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--workload", choices=("cfg1", "cfg2", "cfg3"), default="cfg1")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the DFS hot path is benchmarked on a single MI355X "
@@ -220,6 +344,10 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.workload != "cfg1":
+        line = run_cfg2(args) if args.workload == "cfg2" else run_cfg3(args)
+        print(json.dumps(line), flush=True)
         return
     res = run_gpu(args)
     inputs = res.pop("inputs")

@@ -171,7 +171,9 @@ __global__ void __launch_bounds__(256) score_topk_kernel(ScoreParams p) {
   const int h = blockIdx.y;
   const int qb0 = blockIdx.x * G;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int score_rows = min(pol.scored_rows, pol.dense_row);
+  // Rows from dense_row on keep every column; their scores are only needed
+  // when the caller asks for the score matrix.
+  const int score_rows = p.scores_out ? pol.scored_rows : min(pol.scored_rows, pol.dense_row);
   const bool do_score = qb0 < score_rows;
 
   if (do_score) {

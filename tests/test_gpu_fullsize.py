@@ -1,0 +1,83 @@
+"""Full-size parity at the benchmark shapes (configs[1] Wan, configs[2]
+HunyuanVideo) through properties that do not need a full CPU reference:
+per-row kept-block counts and the policy's dense rows/columns over every
+head, fp32 block scores of one head against the oracle, the selection
+bit-exact from the GPU's own fp32 scores, and sampled query blocks of the
+output against fp32 masked attention on the host."""
+import pytest
+import torch
+
+from oracle import dfs_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(out, ref):
+    return float((out.double() - ref.double()).abs().mean() / ref.double().abs().mean())
+
+
+@pytest.mark.parametrize("cfg_id", [1, 2])
+def test_full_size_call(dev, cfg_id):
+    from dfsattn_amd import ops
+    from dfsattn_amd.layout import ScoringLayout, hunyuan_policy, topk_count, wan_policy
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[cfg_id]
+    hy = cfg.text_len > 0
+    if hy:
+        from dfsattn_amd.attention_hyvideo import DFS_Attention, _dfs_attention_instances, dfs_attention
+    else:
+        from dfsattn_amd.attention_wan import DFS_Attention, _dfs_attention_instances, dfs_attention
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()
+    q, k, v = synth_qkv(cfg, device=dev)
+    perm = hilbert3d_perm(*cfg.grid)
+    kw = dict(video_len=cfg.video_len) if hy else {}
+    step = 12 if hy else 24
+    out = dfs_attention(q, k, v, step_idx=step, skip_steps=12, cache_interval=12, layer_idx=0,
+                        sparsity=cfg.sparsity, sparsity_dcrt=0.0, tile_size=cfg.tile, video_perm=perm, **kw)
+    torch.cuda.synchronize()
+    entry = next(iter(DFS_Attention._cached_metadata.values()))
+    L, H = cfg.seq_len, cfg.heads
+    lay = ScoringLayout(L, cfg.video_len if hy else L, cfg.tile)
+    pol = hunyuan_policy(lay, cfg.sparsity) if hy else wan_policy(lay, cfg.sparsity)
+    counts = (entry["row_ptr"][1:] - entry["row_ptr"][:-1]).view(H, lay.q_blocks).cpu()
+    mask = entry["block_mask"].cpu()
+    kb = lay.k_blocks
+    if hy:
+        ds = cfg.video_len // 128
+        assert bool(mask[:, :, ds:].all()) and bool(mask[:, ds:, :].all())
+        assert bool((counts[:, :ds] == topk_count(cfg.sparsity, kb)).all())
+        assert bool((counts[:, ds:] == kb).all())
+    else:
+        assert bool((counts == topk_count(cfg.sparsity, kb)).all())
+    assert bool((mask.sum(-1) == counts).all())
+
+    # scores of head 0 against the oracle; selection exact from the GPU's own scores
+    full, _ = orc.full_permutation(perm, L)
+    perm_d = ops.device_perm(full, dev)
+    prep = ops.prepare_qkv(q[:, :1], k[:, :1], v[:, :1], perm_d, lay)
+    row_ptr1 = torch.from_numpy(pol.row_ptr(1)).to(dev)
+    col1, scores1, _ = ops.block_score_topk(prep, pol, row_ptr1, want_scores=True)
+    qp = orc.apply_permutation(q[:, :1].float().cpu(), full)
+    kp = orc.apply_permutation(k[:, :1].float().cpu(), full)
+    ref_scores = orc.block_scores(qp, kp, cfg.tile, 128, cfg.video_len if hy else None, head_chunk=1)
+    torch.testing.assert_close(scores1.cpu(), ref_scores, rtol=2e-3, atol=1e-6)
+    got = scores1.cpu()
+    sel = (orc.mask_from_scores_hunyuan(got, cfg.sparsity, L, cfg.video_len) if hy
+           else orc.mask_from_scores_wan(got, cfg.sparsity))
+    assert torch.equal(mask[:1], sel)
+
+    # sampled query blocks of heads 0 and H-1 against fp32 masked attention
+    heads = [0, H - 1]
+    qbs = [0, 1, lay.q_blocks // 2, lay.q_blocks - 2, lay.q_blocks - 1]
+    sub = [orc.apply_permutation(t[:, heads].float().cpu(), full) for t in (q, k, v)]
+    ref = orc.masked_attention(*sub, mask[heads], 128, q_blocks=qbs)
+    got_out = out[:, heads].cpu()[:, :, full]  # execution order
+    rows = torch.cat([torch.arange(b * 128, min((b + 1) * 128, L)) for b in qbs])
+    g, r = got_out[:, :, rows].float(), ref[:, :, rows]
+    assert float((g - r).abs().max()) < 2e-2
+    assert _rel(g, r) < 4e-3  # includes the bf16 rounding of the output
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()

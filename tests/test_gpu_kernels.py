@@ -138,7 +138,8 @@ def test_topk_from_scores_hunyuan_policy(dev, video, text, ratio):
 
 @pytest.mark.parametrize("d,tile,video,text", [(128, 16, 4 * 16 * 16, 0), (128, 16, 3 * 20 * 21, 0),
                                                (64, 16, 4 * 16 * 16, 0), (128, 32, 2000, 0),
-                                               (128, 16, 2000, 100), (64, 32, 1500, 100)])
+                                               (128, 16, 2000, 100), (64, 32, 1500, 100),
+                                               (128, 16, 20 * 128 + 16, 120)])  # last scored row dense, alone in its group
 def test_block_score_topk_matches_oracle(dev, d, tile, video, text):
     from dfsattn_amd.workloads import DfsConfig, synth_qkv
     heads = 2
