@@ -14,6 +14,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "lds_copy.h"
 
 namespace dfs {
 namespace {
@@ -283,6 +284,173 @@ __global__ void __launch_bounds__(256) score_topk_kernel(ScoreParams p) {
   }
 }
 
+// Wide variant: each of the four waves owns its own 32 query tiles (G = 4 *
+// 32 / TPB query blocks per workgroup) and every 32-tile chunk of pooled keys
+// (hi and lo) is copied once into LDS, double-buffered, for all four waves:
+// a quarter of the key traffic of one workgroup per 32 query tiles. The two
+// passes run as one stream of 2 * nchunks chunk steps with one barrier each.
+template <int D, int TPB>
+__global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) {
+  constexpr int CPR = D / 8;             // 16-byte chunks per pooled row
+  constexpr int QBW = 32 / TPB;          // query blocks per wave
+  constexpr int G = 4 * QBW;             // query blocks per workgroup
+  constexpr int ROWS = 32;               // key tiles per chunk
+  constexpr int TILE = ROWS * D;         // uint16 elements of one hi (or lo) chunk
+  constexpr int LOADS = ROWS * D * 2 / 4096;  // 16-byte loads per thread per hi (or lo) chunk
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][2][TILE];  // [buffer][hi, lo]
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const Policy& pol = p.pol;
+  float* bsum = smem;                                          // [G][Kb]
+  uint32_t* hist = reinterpret_cast<uint32_t*>(bsum + G * pol.Kb);  // [4][256]
+
+  const int h = blockIdx.y;
+  const int qb0 = blockIdx.x * G;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int score_rows = p.scores_out ? pol.scored_rows : min(pol.scored_rows, pol.dense_row);
+  const int qbw = qb0 + w * QBW;  // first query block of this wave
+
+  if (qb0 < score_rows) {
+    bf16x8 qh[D / 16], ql[D / 16];
+    const int qt = qbw * TPB + l32;
+    const bool qv = qt < p.q_tiles;
+    const int64_t qbase = (static_cast<int64_t>(h) * p.q_tiles + (qv ? qt : 0)) * CPR + hl;
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ++ds) {
+      qh[ds] = __builtin_bit_cast(bf16x8, qv ? p.q_hi[qbase + 2 * ds] : make_uint4(0, 0, 0, 0));
+      ql[ds] = __builtin_bit_cast(bf16x8, qv ? p.q_lo[qbase + 2 * ds] : make_uint4(0, 0, 0, 0));
+    }
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ++ds) asm volatile("" ::"v"(qh[ds]), "v"(ql[ds]));
+    const bool wave_scores = qbw < score_rows;
+    const int nchunks = (p.k_tiles + ROWS - 1) / ROWS;
+    const uint32_t head_bytes = static_cast<uint32_t>(p.k_tiles) * D * 2;
+    const sgpr4 hrs = make_rsrc(p.k_hi + static_cast<int64_t>(h) * p.k_tiles * CPR, head_bytes);
+    const sgpr4 lrs = make_rsrc(p.k_lo + static_cast<int64_t>(h) * p.k_tiles * CPR, head_bytes);
+    const int ws = __builtin_amdgcn_readfirstlane(w);
+    const TileCopy<D * 2> copy(ws, lane);
+    const uint32_t base = lds_addr(&kbuf[0][0][0]);
+    constexpr uint32_t CHUNK_BYTES = ROWS * D * 2;
+    auto issue = [&](int step) {
+      // Past the last step the copy targets the key tiles past the end: they
+      // return zero and fetch nothing, so the wait count stays fixed.
+      const int c = step < 2 * nchunks ? (step < nchunks ? step : step - nchunks) : nchunks;
+      const uint32_t dst = base + static_cast<uint32_t>((step & 1) * 2 * TILE * 2);
+      copy.template issue<LOADS>(hrs, c * CHUNK_BYTES, dst, ws);
+      copy.template issue<LOADS>(lrs, c * CHUNK_BYTES, dst + TILE * 2, ws);
+    };
+    auto chunk_scores = [&](int buf) {
+      const uint16_t* kh = &kbuf[buf][0][0];
+      const uint16_t* kl = &kbuf[buf][1][0];
+      f32x16 acc = {};
+#pragma unroll
+      for (int ds = 0; ds < D / 16; ++ds) {
+        const bf16x8 ah = __builtin_bit_cast(bf16x8, lds_chunk<CPR>(kh, l32, ds * 2 + hl));
+        const bf16x8 al = __builtin_bit_cast(bf16x8, lds_chunk<CPR>(kl, l32, ds * 2 + hl));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[ds], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[ds], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[ds], acc, 0, 0, 0);
+      }
+      return acc;
+    };
+
+    issue(0);
+    // Pass 1: running max and normaliser (log2 domain) of every query tile,
+    // one per lane half.
+    float m = -INFINITY, z = 0.f;
+    for (int c = 0; c < nchunks; ++c) {
+      wait_vmcnt_0();
+      block_barrier();
+      issue(c + 1);
+      if (wave_scores) {
+        const f32x16 acc = chunk_scores(c & 1);
+        float t[16];
+        float cm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const bool kv = c * ROWS + acc_row(r, hl) < p.k_tiles;
+          t[r] = kv ? acc[r] * p.scale_log2 : -INFINITY;
+          cm = fmaxf(cm, t[r]);
+        }
+        const float mn = fmaxf(m, cm);
+        if (mn > -INFINITY) {
+          float sum = 0.f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sum += exp2_fast(t[r] - mn);
+          z = (m > -INFINITY ? z * exp2_fast(m - mn) : 0.f) + sum;
+          m = mn;
+        }
+      }
+    }
+    // Combine the two lane halves (same query tile, different key tiles).
+    const float m_o = __shfl_xor(m, 32), z_o = __shfl_xor(z, 32);
+    const float M = fmaxf(m, m_o);
+    float Z = 0.f;
+    if (m > -INFINITY) Z += z * exp2_fast(m - M);
+    if (m_o > -INFINITY) Z += z_o * exp2_fast(m_o - M);
+    const float invZ = Z > 0.f ? 1.0f / Z : 0.f;
+
+    // Pass 2: tile probabilities summed into 128x128 blocks.
+    for (int c = 0; c < nchunks; ++c) {
+      const int step = nchunks + c;
+      wait_vmcnt_0();
+      block_barrier();
+      issue(step + 1);
+      if (!wave_scores) continue;
+      const f32x16 acc = chunk_scores(step & 1);
+      float pr[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool kv = c * ROWS + acc_row(r, hl) < p.k_tiles;
+        pr[r] = kv ? exp2_fast(acc[r] * p.scale_log2 - M) * invZ : 0.f;
+      }
+      if constexpr (TPB == 8) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          float sum = (pr[4 * b] + pr[4 * b + 1]) + (pr[4 * b + 2] + pr[4 * b + 3]);
+          sum += __shfl_xor(sum, 32);
+          sum += __shfl_xor(sum, 1);
+          sum += __shfl_xor(sum, 2);
+          sum += __shfl_xor(sum, 4);
+          const int kbk = c * 4 + b;
+          if (hl == 0 && (l32 & 7) == 0 && kbk < pol.Kb) bsum[(w * QBW + (l32 >> 3)) * pol.Kb + kbk] = sum;
+        }
+      } else {
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+          float sum = (pr[4 * gg] + pr[4 * gg + 1]) + (pr[4 * gg + 2] + pr[4 * gg + 3]);
+          sum += __shfl_xor(sum, 1);
+          sum += __shfl_xor(sum, 2);
+          const int kbk = c * 8 + 2 * gg + hl;
+          if ((l32 & 3) == 0 && kbk < pol.Kb) bsum[(w * QBW + (l32 >> 2)) * pol.Kb + kbk] = sum;
+        }
+      }
+    }
+    wait_vmcnt_0();  // the trailing (empty) copies have retired
+    __syncthreads();
+    if (p.scores_out) {
+      for (int i = tid; i < G * pol.Kb; i += 256) {
+        const int g = i / pol.Kb, col = i - g * pol.Kb;
+        const int qb = qb0 + g;
+        if (qb < pol.scored_rows)
+          p.scores_out[(static_cast<int64_t>(h) * pol.scored_rows + qb) * pol.Kb + col] = bsum[i];
+      }
+    }
+  }
+
+  for (int g = 0; g < QBW; ++g) {
+    const int qb = qbw + g;
+    if (qb >= pol.Qb) break;
+    const int64_t row = static_cast<int64_t>(h) * pol.Qb + qb;
+    int32_t* cols = p.col_idx + p.row_ptr[row];
+    uint8_t* mrow = p.mask_out ? p.mask_out + row * pol.Kb : nullptr;
+    if (qb >= pol.dense_row || qb >= pol.scored_rows)
+      dense_row(pol.Kb, cols, mrow, lane);
+    else
+      select_row(bsum + (w * QBW + g) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow,
+                 hist + w * 256, lane);
+  }
+}
+
 struct TopkParams {
   const float* scores;  // [H][scored_rows][Kb]
   const int32_t* row_ptr;
@@ -357,6 +525,11 @@ int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
   const size_t smem = (static_cast<size_t>(G) * k_blocks + 512) * sizeof(float) + 4 * 256 * 4;
   DFS_REQUIRE(smem <= 160 * 1024, "%s: k_blocks=%lld needs %zu bytes of LDS (max 163840)", name,
               (long long)k_blocks, smem);
+  // The wide kernel holds 4x the block-sum rows beside 2 x 2 key chunks.
+  const int Gw = 4 * G;
+  const size_t smem_wide = static_cast<size_t>(Gw) * k_blocks * sizeof(float) + 4 * 256 * 4;
+  const size_t static_wide = 2 * 2 * 32 * static_cast<size_t>(head_dim) * 2;
+  const bool wide = smem_wide + static_wide <= 160 * 1024;
   ScoreParams p{};
   p.q_hi = reinterpret_cast<const uint4*>(q_pool_hi);
   p.q_lo = reinterpret_cast<const uint4*>(q_pool_lo);
@@ -373,6 +546,18 @@ int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
   p.k_tiles = static_cast<int>(k_blocks * tpb);
   p.scale_log2 = static_cast<float>(1.4426950408889634 / sqrt(static_cast<double>(head_dim)));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (wide) {
+    dim3 grid(static_cast<unsigned>((q_blocks + Gw - 1) / Gw), static_cast<unsigned>(heads));
+    if (head_dim == 128 && tpb == 8)
+      score_topk_wide_kernel<128, 8><<<grid, 256, smem_wide, s>>>(p);
+    else if (head_dim == 128)
+      score_topk_wide_kernel<128, 4><<<grid, 256, smem_wide, s>>>(p);
+    else if (tpb == 8)
+      score_topk_wide_kernel<64, 8><<<grid, 256, smem_wide, s>>>(p);
+    else
+      score_topk_wide_kernel<64, 4><<<grid, 256, smem_wide, s>>>(p);
+    return check_launch(name);
+  }
   dim3 grid(static_cast<unsigned>((q_blocks + G - 1) / G), static_cast<unsigned>(heads));
   if (head_dim == 128 && tpb == 8)
     score_topk_kernel<128, 8><<<grid, 256, smem, s>>>(p);
