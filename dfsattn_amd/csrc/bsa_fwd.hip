@@ -39,6 +39,7 @@ struct BsaParams {
   int H, L, R, Qb, Kb;
   int sched;   // workgroup order: 0 head-major across XCDs, 1 XCD-contiguous
   int rotate;  // rotated key-block sweep (split schedule)
+  int pair_order;  // partner-first column order (split schedule, default)
   float scale_log2;
   int out_kind;  // 0 bf16, 1 f16, 2 f32
 };
@@ -282,11 +283,75 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
     load_q<D, QkOp>(q, p, h, qrow, hl, qf);
     // Column list of this row into LDS (read back with uniform ds_reads), and
     // Q fragments forced complete here so no wait for them lands in the loop.
-    for (int i = tid; i < end - beg; i += 256) cols[i] = col_idx[beg + i];
+    int n = end - beg;
+    if (p.pair_order) {
+      // Partner-first order: the columns this row shares with its partner row
+      // (query block qb ^ 1, run by the neighbouring workgroup of the same
+      // XCD at about the same time) first, both ascending, then the rest. The
+      // partner fetches the shared key blocks in the same order, so one of
+      // the two reads of each mostly hits L2.
+      const int W = (p.Kb + 31) >> 5;
+      uint32_t* bm = reinterpret_cast<uint32_t*>(cols + p.Kb);  // [own W][partner W]
+      for (int i = tid; i < 2 * W; i += 256) bm[i] = 0u;
+      block_barrier();
+      for (int i = tid; i < n; i += 256) {
+        const int c = col_idx[beg + i];
+        if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) atomicOr(&bm[c >> 5], 1u << (c & 31));
+      }
+      const int qp = qb ^ 1;
+      if (qp < p.Qb) {
+        const int64_t prow = static_cast<int64_t>(h) * p.Qb + qp;
+        const int pbeg = row_ptr[prow];
+        const int pn = min(max(row_ptr[prow + 1] - pbeg, 0), p.Kb);
+        for (int i = tid; i < pn; i += 256) {
+          const int c = col_idx[pbeg + i];
+          if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) atomicOr(&bm[W + (c >> 5)], 1u << (c & 31));
+        }
+      }
+      block_barrier();
+      if (w == 0) {
+        const int per = (W + 63) >> 6;
+        const int w0 = lane * per;
+        int cs = 0, co = 0;
+        for (int j = 0; j < per && w0 + j < W; ++j) {
+          cs += __popc(bm[w0 + j] & bm[W + w0 + j]);
+          co += __popc(bm[w0 + j] & ~bm[W + w0 + j]);
+        }
+        int is = cs, io = co;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int ys = __shfl_up(is, off, 64), yo = __shfl_up(io, off, 64);
+          if (lane >= off) {
+            is += ys;
+            io += yo;
+          }
+        }
+        const int n_shared = __shfl(is, 63, 64);
+        int ps = is - cs, po = n_shared + io - co;
+        for (int j = 0; j < per && w0 + j < W; ++j) {
+          const uint32_t own = bm[w0 + j], par = bm[W + w0 + j];
+          uint32_t x = own & par;
+          while (x) {
+            cols[ps++] = (w0 + j) * 32 + __ffs(x) - 1;
+            x &= x - 1;
+          }
+          x = own & ~par;
+          while (x) {
+            cols[po++] = (w0 + j) * 32 + __ffs(x) - 1;
+            x &= x - 1;
+          }
+        }
+        if (lane == 63) bm[0] = static_cast<uint32_t>(n_shared + io);  // this row's count
+      }
+      block_barrier();
+      n = static_cast<int>(bm[0]);
+      block_barrier();  // bm[0] read by everybody before any later LDS write
+    } else {
+      for (int i = tid; i < n; i += 256) cols[i] = col_idx[beg + i];
+    }
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qf[s]));
     block_barrier();
-    const int n = end - beg;
     // Rotated sweep: the i-th workgroup of an XCD starts at the first kept
     // column >= i * Kb / CONC (CONC = workgroups resident per XCD) and wraps
     // around. Workgroups start 1 / CONC of a sweep apart, so at any moment the
@@ -294,7 +359,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
     // them in L2. The order is a fixed function of the workgroup, so results
     // are deterministic.
     int j0 = 0;
-    if (p.rotate) {
+    if (p.rotate && !p.pair_order) {
       constexpr int CONC = 64;  // 32 CUs per XCD x 2 workgroups per CU
       const int start = static_cast<int>((static_cast<int64_t>(blockIdx.x >> 3) * p.Kb / CONC) % p.Kb);
       int lo = 0, hi = n;  // lower_bound(cols, start)
@@ -738,7 +803,8 @@ void launch_typed(const BsaArgs& a, const BsaParams& p, BsaSchedule sched, hipSt
   if (sched == kDuo && p.Kb <= 4096) return launch_duo<D, QK_F16, PV_F16>(a, p, s);
   const int S = (p.Qb + 7) / 8;
   dim3 grid(static_cast<unsigned>(p.sched == 0 ? 8 * S * p.H : p.H * p.Qb));
-  const size_t smem = static_cast<size_t>(p.Kb) * sizeof(int32_t);
+  const size_t smem = static_cast<size_t>(p.Kb) * sizeof(int32_t) +
+                      (p.pair_order ? static_cast<size_t>(2 * ((p.Kb + 31) / 32)) * sizeof(uint32_t) : 0);
   bsa_fwd_split_kernel<D, QK_F16, PV_F16><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
                                                                  a.out_perm, a.lse, p);
 }
@@ -792,6 +858,10 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   p.out_kind = out_dtype;
   const char* order = getenv("DFSATTN_AMD_BSA_SCHED");
   p.sched = (order && order[0] == '1') ? 1 : 0;
+  const char* po = getenv("DFSATTN_AMD_BSA_ORDER");
+  // DFSATTN_AMD_BSA_ORDER: "pair" (default, partner-first) or "rotate"
+  // (each row's own ascending list from a workgroup-dependent start).
+  p.pair_order = (po && strcmp(po, "rotate") == 0) ? 0 : 1;
   const char* rot = getenv("DFSATTN_AMD_BSA_ROTATE");
   p.rotate = (rot && rot[0] == '0') ? 0 : 1;
   // DFSATTN_AMD_BSA_KERNEL: "split" (default) or "duo".

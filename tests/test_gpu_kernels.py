@@ -182,7 +182,17 @@ def _run_bsa(dev, q, k, v, mask_bool, pv, out_dtype, perm=None):
     return out.cpu()
 
 
-SCHEDULES = ("split", "duo")
+SCHEDULES = ("split", "split+rotate", "duo")
+
+
+def _set_schedule(monkeypatch, schedule):
+    """DFSATTN_AMD_BSA_KERNEL (and DFSATTN_AMD_BSA_ORDER of the split schedule)."""
+    kernel, _, order = schedule.partition("+")
+    monkeypatch.setenv("DFSATTN_AMD_BSA_KERNEL", kernel)
+    if order:
+        monkeypatch.setenv("DFSATTN_AMD_BSA_ORDER", order)
+    else:
+        monkeypatch.delenv("DFSATTN_AMD_BSA_ORDER", raising=False)
 
 
 @pytest.mark.parametrize("schedule", SCHEDULES)
@@ -193,7 +203,7 @@ SCHEDULES = ("split", "duo")
 def test_bsa_fwd_matches_masked_dense(dev, monkeypatch, schedule, d, length, density, pv):
     """Every attention schedule (DFSATTN_AMD_BSA_KERNEL) against fp32 masked
     attention; odd block counts leave the last query-block pair half empty."""
-    monkeypatch.setenv("DFSATTN_AMD_BSA_KERNEL", schedule)
+    _set_schedule(monkeypatch, schedule)
     from dfsattn_amd.workloads import DfsConfig, synth_qkv
     heads = 2
     cfg = DfsConfig("t", (1, 1, length), heads, d, torch.bfloat16, seed=11)
@@ -231,7 +241,7 @@ def test_bsa_fwd_bf16_out_and_fused_unpermute(dev):
 
 @pytest.mark.parametrize("schedule", SCHEDULES)
 def test_empty_rows_give_zero(dev, monkeypatch, schedule):
-    monkeypatch.setenv("DFSATTN_AMD_BSA_KERNEL", schedule)
+    _set_schedule(monkeypatch, schedule)
     heads, d, length = 1, 128, 512
     q, k, v = (torch.randn((1, heads, length, d)).to(torch.bfloat16) for _ in range(3))
     mask = torch.zeros((heads, 4, 4), dtype=torch.bool)
@@ -246,7 +256,7 @@ def test_empty_rows_give_zero(dev, monkeypatch, schedule):
 def test_rows_keeping_only_a_short_tail_block(dev, monkeypatch, schedule):
     """The last block holds 26 keys: a wave whose keys of that block are all
     masked, and which has seen no other key, must contribute nothing."""
-    monkeypatch.setenv("DFSATTN_AMD_BSA_KERNEL", schedule)
+    _set_schedule(monkeypatch, schedule)
     heads, d, length = 2, 128, 1050
     q, k, v = (torch.randn((1, heads, length, d), generator=torch.Generator().manual_seed(s)).to(torch.bfloat16)
                for s in (21, 22, 23))
