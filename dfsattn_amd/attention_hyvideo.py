@@ -138,10 +138,6 @@ def dfs_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, step_idx: i
     if sparse_execution == "flashinfer64":
         raise ValueError("sparse_execution='flashinfer64' is a research backend not provided by this build; "
                          "use 'native'")
-    if flashinfer64_valid_sequence is not None and flashinfer64_valid_sequence != q.shape[2]:
-        raise NotImplementedError(
-            f"{q.shape[2] - flashinfer64_valid_sequence} padding tokens: the native DFS kernels need every "
-            "token of the sequence to be valid")
     if layer_idx not in _dfs_attention_instances:
         _dfs_attention_instances[layer_idx] = DFS_Attention(
             step_idx, layer_idx, sparsity, cache_flag, video_len, video_perm, block_size, tile_size, tile_size,
@@ -159,6 +155,9 @@ def dfs_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, step_idx: i
     attn.residual_candidate_blocks = residual_candidate_blocks
     attn.selector_mode = selector_mode
     attn.fine_top_p = fine_top_p
+    # valid tokens before the padding segment of cu_seqlens [0, valid, L]
+    # (the processor passes it; replace_hyvideo.py:384)
+    attn.valid_sequence = flashinfer64_valid_sequence
     if record_density and not DFS_Attention.record_density:
         DFS_Attention.set_record_density(True)
     return attn.forward(q=q, k=k, v=v, attn_mask=None, causal=False, drop_rate=0.0, cu_seqlens_q=cu_seqlens_q,

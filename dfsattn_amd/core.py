@@ -112,17 +112,22 @@ class DfsCore:
             raise RuntimeError("DFS attention runs on a ROCm GPU (HIP kernels); got " + str(q.device))
 
     @staticmethod
-    def _check_cu_seqlens(cu: Optional[torch.Tensor], seq_len: int) -> None:
-        """The native path covers one sequence: cu_seqlens [0, L] or [0, L, L]
-        (an empty trailing segment, replace_wan.py:248-249). Checked when the
-        tensor lives on the host; device tensors are taken as given."""
+    def _check_cu_seqlens(cu: Optional[torch.Tensor], seq_len: int) -> Optional[int]:
+        """One batch row: cu_seqlens [0, L], [0, L, L] (an empty trailing
+        segment, replace_wan.py:248-249) or [0, valid, L] (a padding segment
+        after the valid tokens, replace_hyvideo.py:221-228). Returns valid
+        when the tensor lives on the host; device tensors are taken as given
+        (the caller passes the valid length separately)."""
         if cu is None or cu.device.type != "cpu":
-            return
+            return None
         vals = [int(x) for x in cu.flatten().tolist()]
-        if vals[0] != 0 or any(x != seq_len for x in vals[1:]):
+        ok = vals[0] == 0 and vals[-1] == seq_len and len(vals) in (2, 3) and all(
+            0 <= a <= b for a, b in zip(vals, vals[1:]))
+        if not ok:
             raise NotImplementedError(
-                f"cu_seqlens {vals}: a padding segment inside the sequence is not supported by the "
-                "native DFS kernels (all tokens must be valid)")
+                f"cu_seqlens {vals}: the native DFS path takes one sequence, optionally followed by one "
+                f"padding segment ([0, L], [0, L, L] or [0, valid, L] with L = {seq_len})")
+        return vals[1]
 
     # --- selection and execution --------------------------------------------
     def _select(self, prep: ops.Prepared, layout: ScoringLayout, sparse_ratio: float,
@@ -139,6 +144,32 @@ class DfsCore:
     def _execute(self, prep: ops.Prepared, entry: MaskEntry, perm: torch.Tensor) -> torch.Tensor:
         return ops.bsa_fwd(prep, entry["row_ptr"], entry["col_idx"], scale=None, out_dtype=prep.dtype,
                            out_perm=perm)
+
+    def _execute_segments(self, q, k, v, entry: MaskEntry, perm: torch.Tensor, valid: int) -> torch.Tensor:
+        """cu_seqlens [0, valid, L] (attention_hyvideo.py:1054-1082): the
+        external kernel runs the valid tokens and the padding tokens as two
+        sequences, each with the same block mask indexed from its own first
+        token (the mask is repeated per sequence). Valid tokens come first in
+        execution order (the permutation moves video tokens only), so the
+        segments are the execution rows [0, valid) and [valid, L)."""
+        seq_len = q.shape[2]
+        mask = entry["block_mask"]
+        outs = []
+        for start, end in ((0, valid), (valid, seq_len)):
+            n = end - start
+            if n <= 0:
+                continue
+            nb = math.ceil(n / self.block_size)
+            sub = mask[:, :nb, :nb].contiguous()
+            row_ptr, col_idx = ops.mask_to_csr(sub)
+            seg_perm = perm[start:end] - start if start else perm[:end]
+            q_s, k_s, v_s = (x[:, :, start:end] for x in (q, k, v))
+            lay = ScoringLayout(n, n, 16, self.block_size)
+            prep = ops.prepare_qkv(q_s, k_s, v_s, seg_perm.contiguous(), lay,
+                                   pv_dtype=pv_dtype_for(q.dtype, self.pv_dtype), pool=False)
+            outs.append(ops.bsa_fwd(prep, row_ptr, col_idx, scale=None, out_dtype=prep.dtype,
+                                    out_perm=seg_perm.contiguous()))
+        return torch.cat(outs, dim=2)
 
     @staticmethod
     def _tile_counts(entry: MaskEntry) -> np.ndarray:
@@ -158,8 +189,16 @@ class DfsCore:
         cls = type(self)
         self._check_call(q, k, v, attn_mask, causal, drop_rate, batch_size)
         seq_len = q.shape[2]
-        self._check_cu_seqlens(cu_seqlens_q, seq_len)
-        self._check_cu_seqlens(cu_seqlens_kv, seq_len)
+        valid_q = self._check_cu_seqlens(cu_seqlens_q, seq_len)
+        valid_kv = self._check_cu_seqlens(cu_seqlens_kv, seq_len)
+        valid = getattr(self, "valid_sequence", None) or valid_q or seq_len
+        if valid_kv is not None and valid_kv != valid:
+            raise NotImplementedError("different query and key segment splits are not supported")
+        if not 0 < valid <= seq_len:
+            raise ValueError(f"valid sequence {valid} outside [1, {seq_len}]")
+        if valid < self._video_len(seq_len):
+            raise ValueError(f"the padding segment starts at {valid}, inside the video "
+                             f"({self._video_len(seq_len)} tokens): only text tokens may be padding")
         device = q.device
         perm = self._device_permutation(seq_len, device)
         layout = self._layout(seq_len)
@@ -181,7 +220,10 @@ class DfsCore:
         if cls.record_density:
             self._record_density(entry, seq_len)
         t_att = rec.start(device)
-        out = self._execute(prep, entry, perm)
+        if valid < seq_len:
+            out = self._execute_segments(q, k, v, entry, perm, valid)
+        else:
+            out = self._execute(prep, entry, perm)
         rec.stop(t_att, phase="attention_execution", step_idx=self.step_idx, layer_idx=self.layer_idx, device=device)
         return out
 

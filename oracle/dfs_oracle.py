@@ -31,6 +31,10 @@ Each function restates the reference (``codesiena/DFSattn``) at the cited
   with an explicit token mask, and equals dense attention for an all-True mask.
   The external kernel's own rounding is parity unpinned (no fixture exists);
   the contract is the fp32 masked-dense closed form.
+* ``segment_attention`` (the varlen call with cu_seqlens [0, valid, L],
+  attention_hyvideo.py:1054-1082): pinned against dense attention under an
+  explicit block-diagonal token mask whose blocks are counted from each
+  segment's start.
 """
 from __future__ import annotations
 
@@ -265,7 +269,7 @@ def masked_attention(q_perm: torch.Tensor, k_perm: torch.Tensor, v_perm: torch.T
                      mask: torch.Tensor, block: int = BLOCK, scale: Optional[float] = None,
                      heads: Optional[list] = None, q_blocks: Optional[list] = None) -> torch.Tensor:
     """fp32 softmax(Q K^T * scale) V where query block i sees the key blocks
-    kept in mask[h, i] (tokens past L excluded). Returns [B, H, L, D] fp32 with
+    kept in mask[h, i] (tokens and mask columns past L excluded). Returns [B, H, L, D] fp32 with
     rows outside the requested heads / query blocks left at zero.
     Rows with no kept block are zero."""
     q = q_perm.float()
@@ -278,7 +282,7 @@ def masked_attention(q_perm: torch.Tensor, k_perm: torch.Tensor, v_perm: torch.T
     heads = range(n_heads) if heads is None else heads
     for h in heads:
         for i in (range(n_blocks) if q_blocks is None else q_blocks):
-            cols = torch.nonzero(mask[h, i]).flatten().tolist()
+            cols = torch.nonzero(mask[h, i, :n_blocks]).flatten().tolist()
             if not cols:
                 continue
             tok = torch.cat([torch.arange(c * block, min((c + 1) * block, seq_len)) for c in cols])
@@ -286,6 +290,21 @@ def masked_attention(q_perm: torch.Tensor, k_perm: torch.Tensor, v_perm: torch.T
             s = (qi @ k[0, h, tok].T) * scale
             p = torch.softmax(s, dim=-1)
             out[0, h, i * block:(i + 1) * block] = p @ v[0, h, tok]
+    return out
+
+
+def segment_attention(q_perm: torch.Tensor, k_perm: torch.Tensor, v_perm: torch.Tensor,
+                      mask: torch.Tensor, cu_seqlens, block: int = BLOCK) -> torch.Tensor:
+    """Varlen block-masked attention (attention_hyvideo.py:1054-1082): each
+    segment [cu[i], cu[i+1]) attends only within itself, under the same block
+    mask indexed from the segment's own first token (the reference repeats
+    ``base_blockmask`` per sequence)."""
+    out = torch.zeros_like(q_perm, dtype=torch.float32)
+    bounds = [int(x) for x in cu_seqlens]
+    for start, end in zip(bounds, bounds[1:]):
+        if end > start:
+            sl = slice(start, end)
+            out[:, :, sl] = masked_attention(q_perm[:, :, sl], k_perm[:, :, sl], v_perm[:, :, sl], mask, block)
     return out
 
 
@@ -312,9 +331,11 @@ def expand_block_mask(mask: torch.Tensor, seq_len: int, block: int = BLOCK) -> t
 
 def dfs_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, video_perm: torch.Tensor,
                             sparse_ratio: float, tile: int, block: int = BLOCK,
-                            video_len: Optional[int] = None):
+                            video_len: Optional[int] = None, valid: Optional[int] = None):
     """Permute, score, select, attend, unpermute. Returns (out fp32 [1,H,L,D]
-    in the original order, bool mask [H,Qb,Kb], fp32 block scores)."""
+    in the original order, bool mask [H,Qb,Kb], fp32 block scores). With
+    ``valid`` < L (cu_seqlens [0, valid, L]) the mask is still selected over
+    the whole sequence and the attention runs per segment."""
     seq_len = q.shape[2]
     perm, inv = full_permutation(video_perm, seq_len)
     qp, kp, vp = apply_permutation(q, perm), apply_permutation(k, perm), apply_permutation(v, perm)
@@ -323,5 +344,8 @@ def dfs_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, v
         mask = mask_from_scores_wan(scores, sparse_ratio)
     else:
         mask = mask_from_scores_hunyuan(scores, sparse_ratio, seq_len, video_len, block)
-    out = masked_attention(qp, kp, vp, mask, block)
+    if valid is None or valid == seq_len:
+        out = masked_attention(qp, kp, vp, mask, block)
+    else:
+        out = segment_attention(qp, kp, vp, mask, [0, valid, seq_len], block)
     return out[:, :, inv, :], mask, scores

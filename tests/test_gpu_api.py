@@ -118,5 +118,49 @@ def test_api_rejects_what_the_native_path_cannot_run(dev):
         dfs_attention(q.float(), q.float(), q.float(), step_idx=100, layer_idx=7, tile_size=16)
     with pytest.raises(ValueError):
         hy_dfs(q, q, q, step_idx=30, layer_idx=2, tile_size=16, video_len=200, block_top_p=0.9)
-    with pytest.raises(NotImplementedError):
-        hy_dfs(q, q, q, step_idx=30, layer_idx=3, tile_size=16, video_len=200, flashinfer64_valid_sequence=250)
+    with pytest.raises(ValueError):  # padding may only cover text tokens
+        hy_dfs(q, q, q, step_idx=30, layer_idx=3, tile_size=16, video_len=200, flashinfer64_valid_sequence=150)
+    cu = torch.tensor([0, 100, 200, 256], dtype=torch.int32)
+    with pytest.raises(NotImplementedError):  # more than one padding segment
+        hy_dfs(q, q, q, step_idx=30, layer_idx=4, tile_size=16, video_len=200, cu_seqlens_q=cu, cu_seqlens_kv=cu)
+
+
+@pytest.mark.parametrize("grid,text_len,pad,via", [((3, 16, 20), 100, 40, "valid"), ((4, 16, 16), 300, 230, "cu"),
+                                                    ((4, 16, 16), 300, 172, "valid")])
+def test_hunyuan_padding_segment_matches_oracle(dev, grid, text_len, pad, via):
+    """cu_seqlens [0, valid, L] (text padding, replace_hyvideo.py:221-228):
+    the mask is selected over the whole sequence, then the valid tokens and
+    the padding tokens attend as two sequences under the same mask indexed
+    from each one's start (attention_hyvideo.py:1054-1082). The valid length
+    comes from flashinfer64_valid_sequence (as the processor passes it) or
+    from host cu_seqlens."""
+    from dfsattn_amd.attention_hyvideo import DFS_Attention, dfs_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+
+    cfg = DfsConfig("hy-pad", grid, 2, 128, torch.bfloat16, text_len=text_len, seed=11)
+    q, k, v = synth_qkv(cfg)
+    perm = hilbert3d_perm(*cfg.grid)
+    L, vl = cfg.seq_len, cfg.video_len
+    valid = L - pad
+    cu = torch.tensor([0, valid, L], dtype=torch.int32)
+    kw = (dict(flashinfer64_valid_sequence=valid, cu_seqlens_q=cu.to(dev), cu_seqlens_kv=cu.to(dev)) if via == "valid"
+          else dict(cu_seqlens_q=cu, cu_seqlens_kv=cu))
+    out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=12, skip_steps=12, cache_interval=12,
+                        layer_idx=0, sparsity=0.5, sparsity_dcrt=0.1, tile_size=16, video_len=vl,
+                        video_perm=perm, max_seqlen_q=valid, max_seqlen_kv=valid, **kw)
+    key = next(iter(DFS_Attention._cached_metadata))
+    mask = DFS_Attention._cached_metadata[key]["block_mask"].cpu()
+    _, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.5, 16, video_len=vl,
+                                                 valid=valid)
+    assert (mask == ref_mask).float().mean() > 0.99
+    p, inv = orc.full_permutation(perm, L)
+    ref = orc.segment_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask, [0, valid, L])
+    ref = ref[:, :, inv]
+    got = out.cpu().float()
+    assert _rel(got[:, :, :valid], ref[:, :, :valid]) < 4e-3
+    assert _rel(got[:, :, valid:], ref[:, :, valid:]) < 4e-3
+    assert float((got - ref).abs().max()) < 2e-2
+    # the padding rows differ from what the single-sequence call gives them
+    whole = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
+    assert _rel(got[:, :, valid:], whole[:, :, valid:]) > 0.05

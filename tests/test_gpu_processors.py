@@ -97,8 +97,12 @@ def test_wan_processor_sparse_step_matches_reference(dev):
     assert _rel(out.cpu(), expect.cpu()) < 1e-2
 
 
+@pytest.mark.parametrize("n_pad", [0, 30])
 @torch.no_grad()
-def test_hunyuan_processor_sparse_step_with_text(dev):
+def test_hunyuan_processor_sparse_step_with_text(dev, n_pad):
+    """n_pad trailing text tokens masked out by attention_mask: the processor
+    passes cu_seqlens [0, valid, L] and the valid length, so valid tokens and
+    padding attend as two sequences (attention_hyvideo.py:1054-1082)."""
     from dfsattn_amd.attention_hyvideo import DFS_Attention
     from dfsattn_amd.replace_hyvideo import HunyuanVideo_DFSAttn_Processor2_0
     from dfsattn_amd.utils.order import hilbert3d_perm
@@ -112,6 +116,8 @@ def test_hunyuan_processor_sparse_step_with_text(dev):
     x = torch.randn(1, video_len, dim, generator=g).to(dev, torch.bfloat16)
     txt = torch.randn(1, n_text, dim, generator=g).to(dev, torch.bfloat16)
     mask = torch.ones(video_len + n_text, dtype=torch.bool, device=dev)
+    if n_pad:
+        mask[-n_pad:] = False
     hs, enc = proc(attn, x, encoder_hidden_states=txt, attention_mask=mask)
     joint = torch.cat([x, txt], dim=1)
     q = attn.norm_q(attn.to_q(joint).unflatten(2, (heads, -1)).transpose(1, 2)).cpu().float()
@@ -120,8 +126,9 @@ def test_hunyuan_processor_sparse_step_with_text(dev):
     key = next(iter(DFS_Attention._cached_metadata))
     bmask = DFS_Attention._cached_metadata[key]["block_mask"].cpu()
     p, inv = orc.full_permutation(perm, video_len + n_text)
-    ref = orc.masked_attention(*(orc.apply_permutation(t, p) for t in (q, k, v)), bmask)[:, :, inv]
-    ref = ref.transpose(1, 2).flatten(2, 3).to(dev, torch.bfloat16)
+    L = video_len + n_text
+    ref = orc.segment_attention(*(orc.apply_permutation(t, p) for t in (q, k, v)), bmask, [0, L - n_pad, L])
+    ref = ref[:, :, inv].transpose(1, 2).flatten(2, 3).to(dev, torch.bfloat16)
     exp_hs = attn.to_out[0](ref[:, :video_len])
     exp_enc = ref[:, video_len:]
     assert _rel(hs.cpu(), exp_hs.cpu()) < 1e-2

@@ -107,3 +107,17 @@ def test_flop_counts_use_valid_token_blocks():
     assert csr_flops(ptr, cols, 2, 300, 64) == block_flops(mask, 300, 64)
     # cfg 1 nominal bound 35.10 TFLOP
     assert abs(4 * 128 * 128 * 128 * 4184280 / 1e12 - 35.10) < 0.01
+
+
+def test_cu_seqlens_forms():
+    """[0, L], [0, L, L] and [0, valid, L] give the valid length; other
+    splits are refused; device tensors are not read back."""
+    from dfsattn_amd.core import DfsCore
+    check = DfsCore._check_cu_seqlens
+    assert check(None, 300) is None
+    assert check(torch.tensor([0, 300], dtype=torch.int32), 300) == 300
+    assert check(torch.tensor([0, 300, 300], dtype=torch.int32), 300) == 300
+    assert check(torch.tensor([0, 250, 300], dtype=torch.int32), 300) == 250
+    for bad in ([0, 100, 200, 300], [1, 300], [0, 310, 300], [0, 200]):
+        with pytest.raises(NotImplementedError):
+            check(torch.tensor(bad, dtype=torch.int32), 300)

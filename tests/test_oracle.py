@@ -146,6 +146,22 @@ def test_masked_attention_matches_dense_closed_form():
     assert torch.allclose(orc.masked_attention(q, k, v, full), orc.dense_attention(q, k, v), atol=1e-5)
 
 
+def test_segment_attention_matches_block_diagonal_closed_form():
+    """cu_seqlens [0, 300, 430]: the second segment uses mask blocks counted
+    from its own first token (token 300 sits in block 0 of that segment)."""
+    torch.manual_seed(5)
+    q, k, v = (torch.randn(1, 2, 430, 16) for _ in range(3))
+    mask = torch.rand(2, 4, 4) < 0.5
+    mask[:, :, 0] = True
+    got = orc.segment_attention(q, k, v, mask, [0, 300, 430])
+    tok = torch.zeros(2, 430, 430, dtype=torch.bool)
+    tok[:, :300, :300] = orc.expand_block_mask(mask, 300)
+    tok[:, 300:, 300:] = orc.expand_block_mask(mask, 130)
+    assert torch.allclose(got, orc.dense_attention(q, k, v, tok), atol=1e-5)
+    # a single segment is plain masked attention; an empty trailing one adds nothing
+    assert torch.allclose(orc.segment_attention(q, k, v, mask, [0, 430, 430]), orc.masked_attention(q, k, v, mask))
+
+
 def test_full_reference_call_is_permutation_consistent():
     torch.manual_seed(4)
     q, k, v = (torch.randn(1, 2, 256, 16) for _ in range(3))
