@@ -97,6 +97,124 @@ def hilbert3d_perm(f: int, h: int, w: int) -> np.ndarray:
 
 
 # --------------------------------------------------------------------------
+# Other token orders (dfsattn/utils/order.py:8-203, 260-436): per-token loops
+# --------------------------------------------------------------------------
+
+def _gilbert_region(x, y, ax, ay, bx, by):
+    """Published recursive gilbert2d (J. Cervený), one region."""
+    sgn = lambda v: (v > 0) - (v < 0)  # noqa: E731
+    w, h = abs(ax + ay), abs(bx + by)
+    dax, day, dbx, dby = sgn(ax), sgn(ay), sgn(bx), sgn(by)
+    if h == 1:
+        for _ in range(w):
+            yield x, y
+            x, y = x + dax, y + day
+        return
+    if w == 1:
+        for _ in range(h):
+            yield x, y
+            x, y = x + dbx, y + dby
+        return
+    ax2, ay2, bx2, by2 = ax // 2, ay // 2, bx // 2, by // 2
+    w2, h2 = abs(ax2 + ay2), abs(bx2 + by2)
+    if 2 * w > 3 * h:
+        if w2 % 2 and w > 2:
+            ax2, ay2 = ax2 + dax, ay2 + day
+        yield from _gilbert_region(x, y, ax2, ay2, bx, by)
+        yield from _gilbert_region(x + ax2, y + ay2, ax - ax2, ay - ay2, bx, by)
+    else:
+        if h2 % 2 and h > 2:
+            bx2, by2 = bx2 + dbx, by2 + dby
+        yield from _gilbert_region(x, y, bx2, by2, ax2, ay2)
+        yield from _gilbert_region(x + bx2, y + by2, ax, ay, bx - bx2, by - by2)
+        yield from _gilbert_region(x + (ax - dax) + (bx2 - dbx), y + (ay - day) + (by2 - dby),
+                                   -bx2, -by2, -(ax - ax2), -(ay - ay2))
+
+
+def gilbert2d(width: int, height: int):
+    """order.py:8-72: (x, y) cells along the generalised Hilbert curve."""
+    if width >= height:
+        return list(_gilbert_region(0, 0, width, 0, 0, height))
+    return list(_gilbert_region(0, 0, 0, height, width, 0))
+
+
+def hilbert_d2xy(n: int, d: int):
+    """Textbook Hilbert curve on an n x n grid (n a power of two): the d-th
+    cell (x, y), starting at (0, 0) and ending at (n - 1, 0)."""
+    x = y = 0
+    s, t = 1, d
+    while s < n:
+        rx = 1 & (t // 2)
+        ry = 1 & (t ^ rx)
+        if ry == 0:
+            if rx == 1:
+                x, y = s - 1 - x, s - 1 - y
+            x, y = y, x
+        x, y = x + s * rx, y + s * ry
+        t //= 4
+        s *= 2
+    return x, y
+
+
+def hilbert2d_perm(f: int, h: int, w: int) -> np.ndarray:
+    """order.py:75-90."""
+    frame = [y * w + x for x, y in gilbert2d(w, h)]
+    return np.array([z * h * w + i for z in range(f) for i in frame], dtype=np.int64)
+
+
+def _morton_less(a, b):
+    """Morton order without building codes (T. Chan's most-significant-bit
+    comparison): the coordinate whose XOR has the highest set bit decides;
+    on equal highest bits the later axis wins, as it holds the higher bit of
+    each interleaved group."""
+    def msb_less(u, v):
+        return u < v and u < (u ^ v)
+    axis, top = len(a) - 1, a[-1] ^ b[-1]
+    for k in range(len(a) - 2, -1, -1):
+        d = a[k] ^ b[k]
+        if msb_less(top, d):
+            axis, top = k, d
+    return (a[axis] > b[axis]) - (a[axis] < b[axis])
+
+
+def morton_perm(f: int, h: int, w: int, per_frame: bool) -> np.ndarray:
+    """order.py:139-203: Morton order of (x, y, z) over all tokens, or of
+    (x, y) within each frame with frames in order (``per_frame``)."""
+    from functools import cmp_to_key
+    if per_frame:
+        cells = sorted(((x, y) for y in range(h) for x in range(w)), key=cmp_to_key(_morton_less))
+        return np.array([z * h * w + y * w + x for z in range(f) for x, y in cells], dtype=np.int64)
+    pts = sorted(((x, y, z) for z in range(f) for y in range(h) for x in range(w)), key=cmp_to_key(_morton_less))
+    return np.array([z * h * w + y * w + x for x, y, z in pts], dtype=np.int64)
+
+
+def axis_order_perm(f: int, h: int, w: int, target: str) -> np.ndarray:
+    """order.py:260-354: perm[target_index] = original index for the target
+    axis order "hwf" (y*(w*f) + x*f + z) or "fwh" (z*(w*h) + x*h + y)."""
+    perm = np.zeros(f * h * w, dtype=np.int64)
+    for z in range(f):
+        for y in range(h):
+            for x in range(w):
+                t = y * (w * f) + x * f + z if target == "hwf" else z * (w * h) + x * h + y
+                perm[t] = z * h * w + y * w + x
+    return perm
+
+
+def block3d_perm(f: int, h: int, w: int, a: int, b: int, c: int) -> np.ndarray:
+    """order.py:357-436: bricks in (z, y, x) order, tokens of a brick in
+    (z, y, x) order."""
+    out = []
+    for bz in range(0, f, a):
+        for by in range(0, h, b):
+            for bx in range(0, w, c):
+                for z in range(bz, min(bz + a, f)):
+                    for y in range(by, min(by + b, h)):
+                        for x in range(bx, min(bx + c, w)):
+                            out.append(z * h * w + y * w + x)
+    return np.array(out, dtype=np.int64)
+
+
+# --------------------------------------------------------------------------
 # a4: refresh schedule (attention_wan.py:41-66 == attention_hyvideo.py:40-65)
 # --------------------------------------------------------------------------
 

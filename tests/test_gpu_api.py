@@ -164,3 +164,28 @@ def test_hunyuan_padding_segment_matches_oracle(dev, grid, text_len, pad, via):
     # the padding rows differ from what the single-sequence call gives them
     whole = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
     assert _rel(got[:, :, valid:], whole[:, :, valid:]) > 0.05
+
+
+@pytest.mark.parametrize("order", ["org", "morton", "blk", "hwf", "fwh", "hilbert2d"])
+def test_wan_other_token_orders_match_oracle(dev, order):
+    """Every --order of the drivers (wan21_t2v_inference.py:133-144,
+    hyvideo_t2v_inference.py:243-254) through the same native path: the
+    mask and output follow the oracle's whole call under that permutation
+    ("org" passes no permutation)."""
+    from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention
+    from dfsattn_amd.utils.order import video_perm_for
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+
+    cfg = DfsConfig("orders", (3, 16, 20), 2, 128, torch.bfloat16, seed=13)
+    q, k, v = synth_qkv(cfg)
+    perm = video_perm_for(order, *cfg.grid)
+    out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=24, skip_steps=12, cache_interval=12,
+                        layer_idx=0, sparsity=0.3, sparsity_dcrt=0.1, tile_size=16, video_perm=perm)
+    ref_perm = torch.arange(cfg.seq_len) if perm is None else perm
+    _, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), ref_perm, 0.3, 16)
+    mask = DFS_Attention._cached_metadata[(0, "native", 128, 16, 16)]["block_mask"].cpu()
+    assert (mask == ref_mask).float().mean() > 0.99
+    p, inv = orc.full_permutation(ref_perm, cfg.seq_len)
+    ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
+    assert _rel(out.cpu(), ref) < 4e-3
+    assert float((out.cpu().float() - ref).abs().max()) < 2e-2

@@ -121,3 +121,35 @@ def test_cu_seqlens_forms():
     for bad in ([0, 100, 200, 300], [1, 300], [0, 310, 300], [0, 200]):
         with pytest.raises(NotImplementedError):
             check(torch.tensor(bad, dtype=torch.int32), 300)
+
+
+@pytest.mark.parametrize("grid", [(1, 4, 4), (3, 5, 7), (2, 8, 8), (5, 3, 9), (1, 1, 1), (4, 16, 16), (2, 45, 80)])
+def test_token_orders_match_oracle(grid):
+    from dfsattn_amd.utils import order as od
+    f, h, w = grid
+    cases = {
+        "hilbert2d": (od.hilbert2d_perm(f, h, w), orc.hilbert2d_perm(f, h, w)),
+        "morton3d": (od.morton3d_perm(f, h, w), orc.morton_perm(f, h, w, per_frame=False)),
+        "morton2d": (od.morton2d_perm(f, h, w), orc.morton_perm(f, h, w, per_frame=True)),
+        "hwf": (od.hwf(f, h, w), orc.axis_order_perm(f, h, w, "hwf")),
+        "fwh": (od.fwh(f, h, w), orc.axis_order_perm(f, h, w, "fwh")),
+        "blk": (od.block3d_perm(f, h, w, 4, 4, 4), orc.block3d_perm(f, h, w, 4, 4, 4)),
+        "blk_ragged": (od.block3d_perm(f, h, w, 2, 3, 5), orc.block3d_perm(f, h, w, 2, 3, 5)),
+    }
+    for name, (got, ref) in cases.items():
+        assert got.dtype == torch.long and np.array_equal(got.numpy(), ref), name
+
+
+def test_morton_bit_spreading_and_dispatch():
+    from dfsattn_amd.utils import order as od
+    v = torch.tensor([0, 1, 2, 3, 7, (1 << 20), (1 << 21) + 5])
+    assert od.part1by2_tensor(v).tolist() == [0, 1, 8, 9, 0b1001001, 1 << 60, 0b1000001]
+    assert od.part1by1_tensor(torch.tensor([1, 2, 3, (1 << 31), (1 << 32) + 1])).tolist() == [1, 4, 5, 1 << 62, 1]
+    assert od.morton3D_tensor(torch.tensor([1, 0, 0]), torch.tensor([0, 1, 0]), torch.tensor([0, 0, 1])).tolist() == [1, 2, 4]
+    assert od.video_perm_for("org", 2, 3, 4) is None
+    for name in od.ORDERS[1:]:
+        p = od.video_perm_for(name, 3, 8, 8)
+        assert sorted(p.tolist()) == list(range(192)), name
+    assert torch.equal(od.video_perm_for("blk", 3, 8, 8), od.block3d_perm(3, 8, 8, 4, 4, 4))
+    with pytest.raises(ValueError):
+        od.video_perm_for("zigzag", 1, 2, 2)

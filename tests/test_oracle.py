@@ -169,3 +169,44 @@ def test_full_reference_call_is_permutation_consistent():
     out, mask, scores = orc.dfs_attention_reference(q, k, v, perm, 1.0, 16)
     assert mask.all()
     assert torch.allclose(out, orc.dense_attention(q, k, v), atol=1e-5)
+
+
+# ---- other token orders (order.py:8-436)
+@pytest.mark.parametrize("w,h", [(2, 2), (4, 4), (16, 16), (80, 45), (45, 80), (7, 3), (6, 5), (1, 9), (9, 1)])
+def test_gilbert_oracle_invariants(w, h):
+    """Bijection over the rectangle, starts at the origin, unit steps (the
+    generalised curve allows one diagonal step on some even x odd shapes)."""
+    cells = orc.gilbert2d(w, h)
+    assert sorted(cells) == [(x, y) for x in range(w) for y in range(h)]
+    assert cells[0] == (0, 0)
+    steps = [(abs(b[0] - a[0]), abs(b[1] - a[1])) for a, b in zip(cells, cells[1:])]
+    assert all(s in ((1, 0), (0, 1), (1, 1)) for s in steps)
+    assert sum(s == (1, 1) for s in steps) <= 1
+
+
+@pytest.mark.parametrize("n", [2, 4, 8, 32])
+def test_gilbert_oracle_is_the_hilbert_curve_on_power_of_two_squares(n):
+    assert orc.gilbert2d(n, n) == [orc.hilbert_d2xy(n, d) for d in range(n * n)]
+
+
+def test_morton_oracle_against_hand_codes():
+    """Order of 2x2x2 and a 4x4 frame written out by hand from the
+    interleave x0 y0 z0 x1 y1 z1 ... (x lowest)."""
+    cube = orc.morton_perm(2, 2, 2, per_frame=False)
+    # (x, y, z) by code 0..7: (0,0,0) (1,0,0) (0,1,0) (1,1,0) (0,0,1) ... -> z*4 + y*2 + x
+    assert cube.tolist() == [0, 1, 2, 3, 4, 5, 6, 7]
+    frame = orc.morton_perm(1, 4, 4, per_frame=True)
+    assert frame.tolist() == [0, 1, 4, 5, 2, 3, 6, 7, 8, 9, 12, 13, 10, 11, 14, 15]
+    flat = orc.morton_perm(1, 2, 4, per_frame=False)  # x up to 3, y up to 1, z = 0
+    assert flat.tolist() == [0, 1, 4, 5, 2, 3, 6, 7]
+
+
+def test_axis_and_block_oracles_closed_forms():
+    f, h, w = 3, 4, 5
+    hwf = orc.axis_order_perm(f, h, w, "hwf")
+    assert hwf.tolist() == [z * h * w + y * w + x for y in range(h) for x in range(w) for z in range(f)]
+    fwh = orc.axis_order_perm(f, h, w, "fwh")
+    assert fwh.tolist() == [z * h * w + y * w + x for z in range(f) for x in range(w) for y in range(h)]
+    blk = orc.block3d_perm(2, 2, 4, 1, 2, 2)  # bricks of 1x2x2 over a 2x2x4 grid
+    assert blk.tolist() == [0, 1, 4, 5, 2, 3, 6, 7, 8, 9, 12, 13, 10, 11, 14, 15]
+    assert sorted(orc.block3d_perm(5, 3, 9, 4, 4, 4).tolist()) == list(range(135))
