@@ -71,15 +71,39 @@ class AttentionTimingRecorder:
             out.append({"phase": r.phase, "step_idx": r.step_idx, "layer_idx": r.layer_idx, "elapsed_ms": ms})
         return out
 
+    # Phases of the reference's CSV besides the two this build records: its
+    # research executors time these sub-phases (timing.py:113-138). They are
+    # written with zero calls so the file has the same rows.
+    DETAILED_PHASES = (
+        "flashinfer_qkv_permute", "flashinfer_fine_score", "flashinfer_fine_topk", "flashinfer_core_score",
+        "flashinfer_core_select", "flashinfer_occupancy", "flashinfer_partition", "flashinfer_residual_select",
+        "flashinfer_peak_score", "flashinfer_promotion", "flashinfer_residual_compact", "flashinfer_plan",
+        "flashinfer_core_csr_expand", "flashinfer_core_run", "flashinfer_residual_micro_run",
+        "flashinfer_residual_rode_plan", "flashinfer_residual_rode_fp32", "flashinfer_residual_rode_sddmm",
+        "flashinfer_residual_rode_softmax", "flashinfer_residual_rode_spmm", "flashinfer_residual_rode_run",
+        "flashinfer_density_accounting", "flashinfer_lse_merge", "flashinfer_output_unpermute",
+    )
+    METRIC_FIELDS = ("residual_count_mean", "residual_count_p50", "residual_count_p95", "residual_count_max",
+                     "residual_count_nonempty_ratio", "fine_top_k", "occupancy_threshold", "occupancy_mean")
+
     def dump_csv(self, output_path: str, extra_totals: Optional[Dict[str, float]] = None
                  ) -> Dict[str, Dict[str, float]]:
-        """One aggregate row per phase: ``top_k_selection`` (sum of
-        ``topk_mask`` events) and ``attention_execution``, plus extra totals."""
+        """One aggregate row per phase (timing.py:97-218): ``top_k_selection``
+        (sum of ``topk_mask`` events), ``attention_execution``, the detailed
+        phases, any ``extra_totals``, then a ``residual_route_stats`` row when
+        metrics were recorded. Columns: phase, total_ms, calls, mean_ms and
+        the metric fields."""
         totals: Dict[str, float] = {"top_k_selection": 0.0, "attention_execution": 0.0}
+        totals.update({p: 0.0 for p in self.DETAILED_PHASES})
         calls: Dict[str, float] = {p: 0.0 for p in totals}
         aliases = {"topk_mask": "top_k_selection", "attention_execution": "attention_execution"}
         for row in self.rows():
-            phase = aliases.get(row["phase"])
+            raw = row["phase"]
+            phase = aliases.get(raw)
+            if phase is None and (raw in self.DETAILED_PHASES or raw.startswith("flashinfer_residual_bucket_le")):
+                phase = raw
+                totals.setdefault(phase, 0.0)
+                calls.setdefault(phase, 0.0)
             if phase is None:
                 continue
             totals[phase] += float(row["elapsed_ms"])
@@ -89,11 +113,16 @@ class AttentionTimingRecorder:
             calls[phase] = 1.0
         os.makedirs(os.path.dirname(output_path) or ".", exist_ok=True)
         with open(output_path, "w", newline="") as fh:
-            wr = csv.DictWriter(fh, fieldnames=["phase", "total_ms", "calls", "mean_ms"])
+            wr = csv.DictWriter(fh, fieldnames=["phase", "total_ms", "calls", "mean_ms", *self.METRIC_FIELDS])
             wr.writeheader()
             for phase, total in totals.items():
                 n = calls.get(phase, 0.0)
                 wr.writerow({"phase": phase, "total_ms": total, "calls": int(n),
                              "mean_ms": total / n if n else 0.0})
+            metrics = {name: self._metric_records.get(name, []) for name in self.METRIC_FIELDS}
+            n_metric = max((len(v) for v in metrics.values()), default=0)
+            if n_metric:
+                wr.writerow({"phase": "residual_route_stats", "total_ms": "", "calls": n_metric, "mean_ms": "",
+                             **{k: sum(v) / len(v) if v else float("nan") for k, v in metrics.items()}})
         return {p: {"calls": calls.get(p, 0.0), "total_ms": t, "mean_ms": t / calls[p] if calls.get(p) else 0.0}
                 for p, t in totals.items()}

@@ -189,3 +189,37 @@ def test_wan_other_token_orders_match_oracle(dev, order):
     ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
     assert _rel(out.cpu(), ref) < 4e-3
     assert float((out.cpu().float() - ref).abs().max()) < 2e-2
+
+
+def test_records_and_mask_export_from_a_call(dev, tmp_path):
+    """record_density, record_timing and configure_mask_export around one
+    refresh call: the density is the kept fraction of the cached mask, the
+    exported npy equals it, and the timing CSV counts one selection and one
+    execution."""
+    import csv
+
+    import numpy as np
+    from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[0]
+    q, k, v = (x.to(dev) for x in synth_qkv(cfg, dtype=torch.bfloat16))
+    DFS_Attention.configure_mask_export(str(tmp_path / "masks"), head_indices=(1,), layer_interval=3, save_bool=True)
+    DFS_Attention.set_record_timing(True)
+    try:
+        dfs_attention(q, k, v, step_idx=24, skip_steps=12, cache_interval=12, layer_idx=3, sparsity=0.3,
+                      sparsity_dcrt=0.1, tile_size=16, video_perm=hilbert3d_perm(*cfg.grid), record_density=True)
+        mask = DFS_Attention._cached_metadata[(3, "native", 128, 16, 16)]["block_mask"].cpu()
+        assert DFS_Attention.get_density_records()[24][3] == pytest.approx(float(mask.float().mean()))
+        layer = tmp_path / "masks" / "step_024" / "layer_03"
+        assert np.array_equal(np.load(layer / "block_mask.npy"), mask.numpy())
+        assert (layer / "head_01_block_mask.png").exists()
+        DFS_Attention.dump_timing_records(str(tmp_path / "timing.csv"))
+        rows = {r["phase"]: r for r in csv.DictReader(open(tmp_path / "timing.csv"))}
+        assert rows["top_k_selection"]["calls"] == "1" and rows["attention_execution"]["calls"] == "1"
+        assert float(rows["attention_execution"]["total_ms"]) > 0
+    finally:
+        DFS_Attention.configure_mask_export(None)
+        DFS_Attention.set_record_timing(False)
+        DFS_Attention.set_record_density(False)

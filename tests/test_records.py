@@ -1,0 +1,86 @@
+"""On-disk and record formats (CPU): block-mask export and heatmaps
+(visualization.py:8-330), the timing CSV (timing.py:97-218) and the
+execution-tile density records (attention_wan.py:576-661)."""
+import csv
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from dfsattn_amd.utils import visualization as vis
+from dfsattn_amd.utils.timing import AttentionTimingRecorder
+
+
+def test_export_block_mask_layout(tmp_path):
+    mask = torch.rand(3, 6, 6, generator=torch.Generator().manual_seed(0)) < 0.4
+    npy, pngs = vis.export_block_mask(mask, str(tmp_path), 12, 3, head_indices=(0, 2), save_bool=True)
+    layer = tmp_path / "step_012" / "layer_03"
+    assert npy == str(layer / "block_mask.npy")
+    saved = np.load(npy, allow_pickle=False)
+    assert saved.dtype == np.bool_ and np.array_equal(saved, mask.numpy())
+    assert pngs == [str(layer / "head_00_block_mask.png"), str(layer / "head_02_block_mask.png")]
+    assert all(os.path.getsize(p) > 0 for p in pngs)
+    npy2, pngs2 = vis.export_block_mask(mask[1], str(tmp_path), 0, 0)  # 2D mask, default head 0, no npy
+    assert npy2 is None and pngs2 == [str(tmp_path / "step_000" / "layer_00" / "head_00_block_mask.png")]
+    with pytest.raises(ValueError):
+        vis.export_block_mask(mask, str(tmp_path), 0, 0, head_indices=(3,))
+    with pytest.raises(ValueError):
+        vis.export_block_mask(mask[None], str(tmp_path), 0, 0)
+
+
+def test_other_heatmaps_are_written(tmp_path):
+    g = torch.Generator().manual_seed(1)
+    attn = torch.softmax(torch.randn(300, 300, generator=g), -1)
+    mask = torch.rand(3, 3, generator=g) < 0.5
+    paths = [vis.attention_map_visualization(attn, str(tmp_path), 1, 2, 0),
+             vis.mask_visualization(mask, str(tmp_path), 1, 2, 0),
+             vis.mask_visualization(mask, str(tmp_path), 1, 2, 0, suffix="dense"),
+             vis.attention_map_with_mask_visualization(attn, mask, str(tmp_path), 1, 2, 0, block_size=128)]
+    names = [os.path.basename(p) for p in paths]
+    assert names == ["head_00.png", "head_00_mask.png", "head_00_mask_dense.png", "head_00_with_mask.png"]
+    assert all(os.path.getsize(p) > 0 for p in paths)
+
+
+def test_timing_csv_rows_and_columns(tmp_path):
+    rec = AttentionTimingRecorder(enabled=True)
+    cpu = torch.device("cpu")
+    for phase in ("topk_mask", "topk_mask", "attention_execution", "qkv_permute", "flashinfer_plan"):
+        rec.stop(rec.start(cpu), phase=phase, step_idx=12, layer_idx=0, device=cpu)
+    rec.record_metrics({"fine_top_k": 4.0})
+    rec.record_metrics({"fine_top_k": 6.0})
+    out = tmp_path / "t" / "timing.csv"
+    summary = rec.dump_csv(str(out), extra_totals={"total_pipeline": 1234.5})
+    rows = list(csv.DictReader(open(out)))
+    assert list(rows[0].keys()) == ["phase", "total_ms", "calls", "mean_ms", *AttentionTimingRecorder.METRIC_FIELDS]
+    phases = [r["phase"] for r in rows]
+    assert phases[:2] == ["top_k_selection", "attention_execution"]
+    assert phases[2:2 + len(AttentionTimingRecorder.DETAILED_PHASES)] == list(AttentionTimingRecorder.DETAILED_PHASES)
+    assert phases[-2:] == ["total_pipeline", "residual_route_stats"]
+    by = {r["phase"]: r for r in rows}
+    assert by["top_k_selection"]["calls"] == "2" and by["attention_execution"]["calls"] == "1"
+    assert by["flashinfer_plan"]["calls"] == "1" and by["flashinfer_core_run"]["calls"] == "0"
+    assert "qkv_permute" not in by  # recorded but not a CSV phase, as in the reference
+    assert float(by["residual_route_stats"]["fine_top_k"]) == 5.0
+    assert summary["total_pipeline"] == {"calls": 1.0, "total_ms": 1234.5, "mean_ms": 1234.5}
+    disabled = AttentionTimingRecorder(enabled=False)
+    assert disabled.start(cpu) is None
+
+
+def test_density_records_csv(tmp_path, capsys):
+    from dfsattn_amd.attention_wan import DFS_Attention
+    DFS_Attention.execution_tile_records.clear()
+    assert DFS_Attention.dump_density_records(str(tmp_path / "none.csv")) is None
+    for step, layer, dens in ((24, 1, 0.25), (24, 0, 0.5), (12, 0, 1.0)):
+        DFS_Attention.execution_tile_records.setdefault(step, {})[layer] = {
+            "execution_backend": "native", "execution_tile_size": 128, "q_tile_rows": 8, "k_tile_cols": 8,
+            "tile_k_mean": 8 * dens, "tile_k_min": 1, "tile_k_max": 8, "tiles_executed": int(64 * dens),
+            "tiles_dense": 64, "execution_tile_density": dens}
+    path = DFS_Attention.dump_density_records(str(tmp_path / "d" / "density.csv"))
+    rows = list(csv.DictReader(open(path)))
+    assert [(r["step_idx"], r["layer_idx"]) for r in rows] == [("12", "0"), ("24", "0"), ("24", "1")]
+    assert list(rows[0].keys())[:4] == ["step_idx", "layer_idx", "execution_backend", "execution_tile_size"]
+    printed = capsys.readouterr().out
+    assert "Mean execution-tile density: 0.5833" in printed
+    assert "Mean per-step execution-tile density: 0.6875" in printed
+    DFS_Attention.execution_tile_records.clear()
