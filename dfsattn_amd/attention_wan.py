@@ -18,7 +18,7 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .core import DfsCore, MaskEntry, pv_dtype_for
+from .core import DfsCore, MaskEntry, operand_dtype_for
 from .layout import ScoringLayout, TopkPolicy, wan_policy
 from .utils.logger import logger
 from .utils.timing import AttentionTimingRecorder

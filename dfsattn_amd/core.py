@@ -57,10 +57,11 @@ class MaskEntry(dict):
         return out
 
 
-def pv_dtype_for(dtype: torch.dtype, requested: Optional[torch.dtype]) -> torch.dtype:
-    """PV operand precision: f16 by default (P rounded to 11 bits keeps the
-    output within 1e-3 mean-rel of fp32); bf16 keeps V's bits exactly and
-    matches the reference kernel's bf16 P, at ~1.5e-3 mean-rel."""
+def operand_dtype_for(dtype: torch.dtype, requested: Optional[torch.dtype]) -> torch.dtype:
+    """Attention operand precision: f16 by default (Q * scale * log2(e), K, V
+    and P rounded to 11 bits keep the output within 1e-3 mean-rel of fp32);
+    bf16 keeps the inputs' bits and runs P in bf16, the reference kernel's
+    precision class (~1.5e-3 mean-rel). f16 inputs always run in f16."""
     if dtype == torch.float16:
         return torch.float16
     return requested or torch.float16
@@ -70,7 +71,7 @@ class DfsCore:
     """Mixin with the device flow; subclasses provide ``_video_len`` and
     ``_policy`` and the class-level state dictionaries."""
 
-    pv_dtype: Optional[torch.dtype] = None  # None -> pv_dtype_for default
+    operand_dtype: Optional[torch.dtype] = None  # None -> operand_dtype_for default
 
     # --- permutation -----------------------------------------------------
     def _device_permutation(self, seq_len: int, device: torch.device) -> torch.Tensor:
@@ -166,7 +167,7 @@ class DfsCore:
             q_s, k_s, v_s = (x[:, :, start:end] for x in (q, k, v))
             lay = ScoringLayout(n, n, 16, self.block_size)
             prep = ops.prepare_qkv(q_s, k_s, v_s, seg_perm.contiguous(), lay,
-                                   pv_dtype=pv_dtype_for(q.dtype, self.pv_dtype), pool=False)
+                                   operand_dtype=operand_dtype_for(q.dtype, self.operand_dtype), pool=False)
             outs.append(ops.bsa_fwd(prep, row_ptr, col_idx, scale=None, out_dtype=prep.dtype,
                                     out_perm=seg_perm.contiguous()))
         return torch.cat(outs, dim=2)
@@ -207,7 +208,7 @@ class DfsCore:
         recompute = entry is None or self.cache_flag
         rec = cls.timing_recorder
         t_perm = rec.start(device)
-        prep = ops.prepare_qkv(q, k, v, perm, layout, pv_dtype=pv_dtype_for(q.dtype, self.pv_dtype), pool=recompute)
+        prep = ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=operand_dtype_for(q.dtype, self.operand_dtype), pool=recompute)
         rec.stop(t_perm, phase="qkv_permute", step_idx=self.step_idx, layer_idx=self.layer_idx, device=device)
         if recompute:
             t_topk = rec.start(device)

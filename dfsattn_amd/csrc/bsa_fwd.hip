@@ -126,7 +126,7 @@ __device__ __forceinline__ void load_q(const uint16_t* __restrict__ q, const Bsa
 // operands of the next 32-key chunk are fetched while this chunk's MFMAs run.
 template <int D, typename QkOp>
 __device__ __forceinline__ void qk_tile(const uint16_t* k_tile, const typename QkOp::vec* qf, int l32, int hl,
-                                        f32x16* s) {
+                                        f32x16* s, const f32x16& init = f32x16{}) {
   constexpr int CPR = D / 8, DS = D / 16;
   uint4 a[2][DS];
 #pragma unroll
@@ -137,7 +137,7 @@ __device__ __forceinline__ void qk_tile(const uint16_t* k_tile, const typename Q
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) a[(kc + 1) & 1][ds] = lds_chunk<CPR>(k_tile, (kc + 1) * 32 + l32, ds * 2 + hl);
     }
-    s[kc] = f32x16{};
+    s[kc] = init;
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds)
       s[kc] = QkOp::run(__builtin_bit_cast(typename QkOp::vec, a[kc & 1][ds]), qf[ds], s[kc]);
@@ -194,6 +194,79 @@ __device__ __forceinline__ void pv_tile(const uint16_t* v_tile, const f32x16* s,
     for (int j = 0; j < 4; ++j) {
       pr[j] = PvOp::pack(exp2_fast(fmaf(src[r0 + 2 * j], scale_log2, -mnew)),
                          exp2_fast(fmaf(src[r0 + 2 * j + 1], scale_log2, -mnew)));
+      lsum = PvOp::sum2(pr[j], lsum);
+    }
+    const typename PvOp::vec pf = __builtin_bit_cast(typename PvOp::vec, pr);
+#pragma unroll
+    for (int dc = 0; dc < DCH; ++dc) {
+      const uint4 a = lds_chunk<16>(v_tile, dc * 32 + l32, ks * 2 + hl);
+      o[dc] = PvOp::run(__builtin_bit_cast(typename PvOp::vec, a), pf, o[dc]);
+    }
+  }
+}
+
+// f16 Q fragments with c = scale * log2(e) folded in (q * c rounded to f16),
+// so that S^T = K (Q c)^T arrives in log2 units.
+template <int D>
+__device__ __forceinline__ void load_q_scaled(const uint16_t* __restrict__ q, const BsaParams& p, int h, int qrow,
+                                              int hl, f16x8* qf) {
+  load_q<D, MfmaOp<true>>(q, p, h, qrow, hl, qf);
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qf[s][i] = static_cast<_Float16>(static_cast<float>(qf[s][i]) * p.scale_log2);
+}
+
+// Lazy online softmax on S' = S c - m, where the running reference m enters
+// through the QK MFMA's C input (negm holds -m in every element). m moves
+// only when some row of the wave sees a block maximum above m + kLazyTau, or
+// on the row's first block, so P = exp2(S') stays <= 2^kLazyTau (f16 holds
+// it exactly to 11 bits) and O and l are rarely rescaled. The result is the
+// same softmax: numerator and denominator share the reference.
+constexpr float kLazyTau = 8.0f;
+template <int DCH>
+__device__ __forceinline__ void softmax_lazy(f32x16* s, bool first, float& m, float& lsum, f32x16* o,
+                                             f32x16& negm) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kc][r]);
+  const float bm = xhalf_max(mx);
+  if (first || __any(bm > kLazyTau)) {
+    float shift = first ? bm : fmaxf(bm, 0.f);
+    if (!(shift > -INFINITY)) shift = 0.f;  // a row with every key masked keeps m
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kc][r] -= shift;
+    if (!first) {
+      const float alpha = exp2_fast(-shift);
+      lsum *= alpha;
+#pragma unroll
+      for (int i = 0; i < DCH; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+    }
+    m += shift;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negm[r] = -m;
+  }
+}
+
+// O^T += V^T P^T with P = exp2(S') (S' already in log2 units relative to m).
+template <int D, typename PvOp>
+__device__ __forceinline__ void pv_tile_log2(const uint16_t* v_tile, const f32x16* s, float& lsum, f32x16* o,
+                                             int l32, int hl) {
+  constexpr int DCH = D / 32;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    const f32x16& src = s[ks >> 1];
+    const int r0 = (ks & 1) * 8;
+    typename PvOp::pair pr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pr[j] = PvOp::pack(exp2_fast(src[r0 + 2 * j]), exp2_fast(src[r0 + 2 * j + 1]));
       lsum = PvOp::sum2(pr[j], lsum);
     }
     const typename PvOp::vec pf = __builtin_bit_cast(typename PvOp::vec, pr);
@@ -269,7 +342,9 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
   f32x16 o[DCH];
 #pragma unroll
   for (int i = 0; i < DCH; ++i) o[i] = f32x16{};
-  float m = -INFINITY, lsum = 0.f;
+  // f16 Q/K: S arrives in log2 units relative to m (lazy softmax); bf16 Q/K:
+  // S is scaled in the exponent and m is the exact running maximum.
+  float m = QK_F16 ? 0.f : -INFINITY, lsum = 0.f;
 
   if (beg < end) {
     const uint32_t head_bytes = static_cast<uint32_t>(p.R) * D * 2;
@@ -280,7 +355,11 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
     const TileCopy<D * 2> kcopy(ws, lane);
     const TileCopy<256> vcopy(ws, lane);
     typename QkOp::vec qf[D / 16];
-    load_q<D, QkOp>(q, p, h, qrow, hl, qf);
+    if constexpr (QK_F16)
+      load_q_scaled<D>(q, p, h, qrow, hl, qf);
+    else
+      load_q<D, QkOp>(q, p, h, qrow, hl, qf);
+    f32x16 negm = f32x16{};  // -m in every element (f16 Q/K)
     // Column list of this row into LDS (read back with uniform ds_reads), and
     // Q fragments forced complete here so no wait for them lands in the loop.
     int n = end - beg;
@@ -387,7 +466,10 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
       wait_vmcnt<V_LOADS>();  // this wave's K copies have landed
       block_barrier();        // ... and everybody else's
       f32x16 s[4];
-      qk_tile<D, QkOp>(k_lds, qf, l32, hl, s);
+      if constexpr (QK_F16)
+        qk_tile<D, QkOp>(k_lds, qf, l32, hl, s, negm);
+      else
+        qk_tile<D, QkOp>(k_lds, qf, l32, hl, s);
       block_barrier();  // K tile fully consumed
       kcopy.template issue<K_LOADS>(krs, kb_next * TILE_BYTES, k_base, ws);
       if (tail_possible && kb == p.Kb - 1) {
@@ -395,10 +477,17 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
         asm volatile("" : "+s"(valid));  // compares stay in this (rare) branch
         mask_tail(s, valid, hl);
       }
-      const float mnew = softmax_max<DCH, true>(s, p.scale_log2, m, lsum, o);
-      wait_vmcnt<K_LOADS>();  // V copies landed (the next K may be in flight)
-      block_barrier();
-      pv_tile<D, PvOp>(v_lds, s, p.scale_log2, mnew, lsum, o, l32, hl);
+      if constexpr (QK_F16) {
+        softmax_lazy<DCH>(s, t == 0, m, lsum, o, negm);
+        wait_vmcnt<K_LOADS>();  // V copies landed (the next K may be in flight)
+        block_barrier();
+        pv_tile_log2<D, PvOp>(v_lds, s, lsum, o, l32, hl);
+      } else {
+        const float mnew = softmax_max<DCH, true>(s, p.scale_log2, m, lsum, o);
+        wait_vmcnt<K_LOADS>();
+        block_barrier();
+        pv_tile<D, PvOp>(v_lds, s, p.scale_log2, mnew, lsum, o, l32, hl);
+      }
       block_barrier();  // V tile fully consumed
       vcopy.template issue<V_LOADS>(vrs, kb_next * TILE_BYTES, v_base, ws);
       kb = kb_next;

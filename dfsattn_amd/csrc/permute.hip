@@ -112,9 +112,22 @@ struct PrepParams {
   int k_tiles;   // pooled key tiles (whole scoring layout)
   int tile;      // tokens per tile
   int in_f16;    // q/k/v are f16 (else bf16)
-  int pv_convert;  // v_t receives bf16 -> f16 converted values
+  int convert;   // bf16 inputs, f16 operands: q_perm, k_perm and v_t get converted values
   int pool;      // write pooled tiles
 };
+
+// bf16 -> f16 of eight packed values; *overflow is set when a finite value
+// exceeds the f16 range.
+__device__ __forceinline__ uint4 bf16x8_to_f16x8(const uint4& v, bool* overflow) {
+  uint32_t e[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float f = bf16_bits_to_f32(u16_at(v, i));
+    e[i] = f32_to_f16_bits(f);
+    *overflow |= ((e[i] & 0x7fffu) == 0x7c00u) && !isinf(f);
+  }
+  return make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+}
 
 // Scoring-layout position -> execution row, or -1 for an inserted zero row.
 __device__ __forceinline__ int scoring_to_exec(int pos, const PrepParams& p) {
@@ -157,16 +170,18 @@ __global__ void __launch_bounds__(256) prep_qk_kernel(PrepParams p) {
   const int c = lane % CPR;
   const int g = lane / CPR;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  bool overflow = false;
   for (int r = g; r < p.tile; r += RPP) {
     const int x = scoring_to_exec(t * p.tile + r, p);
     if (x >= 0) {
       const int s = p.perm[x];
       uint4 val = make_uint4(0, 0, 0, 0);
       if (s >= 0 && s < p.L) val = src[static_cast<int64_t>(s) * CPR + c];
-      dst[static_cast<int64_t>(x) * CPR + c] = val;
-      add_chunk(acc, val, p.in_f16 != 0);
+      dst[static_cast<int64_t>(x) * CPR + c] = p.convert ? bf16x8_to_f16x8(val, &overflow) : val;
+      add_chunk(acc, val, p.in_f16 != 0);  // tile means of the input values
     }
   }
+  if (p.v_overflow && overflow) atomicOr(p.v_overflow, 1);
   const int n_tiles = is_k ? p.k_tiles : p.q_tiles;
   if (!p.pool || t >= n_tiles) return;
 #pragma unroll
@@ -227,7 +242,7 @@ __global__ void __launch_bounds__(16 * (D / 8)) prep_v_kernel(PrepParams p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       uint32_t bits = u16_at(rows[i], j);
-      if (p.pv_convert) {
+      if (p.convert) {
         const float f = bf16_bits_to_f32(bits);
         bits = f32_to_f16_bits(f);
         overflow |= ((bits & 0x7fffu) == 0x7c00u) && !isinf(f);  // finite -> inf
@@ -262,7 +277,7 @@ int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst, int64_t
 
 int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* perm,
                     int64_t heads, int64_t seq_len, int64_t head_dim, int dtype,
-                    int64_t video_len, int64_t tile_size, int pv_dtype, void* q_perm,
+                    int64_t video_len, int64_t tile_size, int operand_dtype, void* q_perm,
                     void* k_perm, void* v_t, uint16_t* q_pool_hi, uint16_t* q_pool_lo,
                     uint16_t* k_pool_hi, uint16_t* k_pool_lo, int32_t* v_overflow,
                     dfs_stream_t stream) {
@@ -272,10 +287,10 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* 
               (long long)head_dim);
   DFS_REQUIRE(dtype == DFS_DTYPE_BF16 || dtype == DFS_DTYPE_F16,
               "dfs_prepare_qkv: dtype=%d (supported: bf16, f16)", dtype);
-  DFS_REQUIRE(pv_dtype == DFS_DTYPE_BF16 || pv_dtype == DFS_DTYPE_F16,
-              "dfs_prepare_qkv: pv_dtype=%d (supported: bf16, f16)", pv_dtype);
-  DFS_REQUIRE(!(dtype == DFS_DTYPE_F16 && pv_dtype == DFS_DTYPE_BF16),
-              "dfs_prepare_qkv: f16 inputs need an f16 PV operand");
+  DFS_REQUIRE(operand_dtype == DFS_DTYPE_BF16 || operand_dtype == DFS_DTYPE_F16,
+              "dfs_prepare_qkv: operand_dtype=%d (supported: bf16, f16)", operand_dtype);
+  DFS_REQUIRE(!(dtype == DFS_DTYPE_F16 && operand_dtype == DFS_DTYPE_BF16),
+              "dfs_prepare_qkv: f16 inputs need f16 operands");
   DFS_REQUIRE(heads > 0 && heads < 65536, "dfs_prepare_qkv: heads=%lld out of range", (long long)heads);
   DFS_REQUIRE(seq_len > 0 && video_len > 0 && video_len <= seq_len,
               "dfs_prepare_qkv: need 0 < video_len=%lld <= seq_len=%lld", (long long)video_len,
@@ -316,7 +331,7 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* 
   p.q_tiles = static_cast<int>(vb * kBlock / tile_size);
   p.k_tiles = static_cast<int>(kb * kBlock / tile_size);
   p.in_f16 = dtype == DFS_DTYPE_F16;
-  p.pv_convert = (dtype == DFS_DTYPE_BF16 && pv_dtype == DFS_DTYPE_F16);
+  p.convert = (dtype == DFS_DTYPE_BF16 && operand_dtype == DFS_DTYPE_F16);
   p.pool = pool ? 1 : 0;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);

@@ -92,8 +92,8 @@ class Prepared:
     layout: ScoringLayout
     heads: int
     head_dim: int
-    dtype: torch.dtype
-    pv_dtype: torch.dtype
+    dtype: torch.dtype          # input dtype (and the default output dtype)
+    operand_dtype: torch.dtype  # dtype of q_perm, k_perm and v_t
     q_perm: torch.Tensor  # [H, R, D]
     k_perm: torch.Tensor  # [H, R, D]
     v_t: torch.Tensor     # [H, R/128, D, 128]
@@ -101,14 +101,17 @@ class Prepared:
     q_lo: Optional[torch.Tensor] = None
     k_hi: Optional[torch.Tensor] = None  # [H, k_tiles, D] bf16
     k_lo: Optional[torch.Tensor] = None
-    v_overflow: Optional[torch.Tensor] = None
+    overflow: Optional[torch.Tensor] = None
 
 
 def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.Tensor,
-                layout: ScoringLayout, pv_dtype: Optional[torch.dtype] = None, pool: bool = True,
+                layout: ScoringLayout, operand_dtype: Optional[torch.dtype] = None, pool: bool = True,
                 check_overflow: bool = False) -> Prepared:
     """Gathers Q, K, V into execution order (V block-transposed) and, with
-    ``pool``, writes the tile means used for scoring."""
+    ``pool``, writes the tile means used for scoring. ``operand_dtype`` (f16
+    by default) is the dtype of the attention operands: f16 rounds bf16
+    inputs to f16; bf16 keeps their bits. ``check_overflow`` allocates a flag
+    set when a finite input exceeds the f16 range."""
     _require_device(q, k, v, perm)
     heads, length, dim = _heads_rows(q)
     if q.dtype not in (torch.bfloat16, torch.float16):
@@ -119,15 +122,17 @@ def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.T
         raise ValueError(f"sequence length {length} does not match the layout ({layout.seq_len})")
     if perm.numel() != length:
         raise ValueError(f"permutation has {perm.numel()} entries for {length} tokens")
-    pv_dtype = pv_dtype or torch.float16
+    operand_dtype = operand_dtype or torch.float16
+    if operand_dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"operand_dtype must be bf16 or f16, got {operand_dtype}")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     dev = q.device
     rows = layout.rows
     prep = Prepared(
-        layout=layout, heads=heads, head_dim=dim, dtype=q.dtype, pv_dtype=pv_dtype,
-        q_perm=torch.empty((heads, rows, dim), dtype=q.dtype, device=dev),
-        k_perm=torch.empty((heads, rows, dim), dtype=q.dtype, device=dev),
-        v_t=torch.empty((heads, rows // 128, dim, 128), dtype=pv_dtype, device=dev),
+        layout=layout, heads=heads, head_dim=dim, dtype=q.dtype, operand_dtype=operand_dtype,
+        q_perm=torch.empty((heads, rows, dim), dtype=operand_dtype, device=dev),
+        k_perm=torch.empty((heads, rows, dim), dtype=operand_dtype, device=dev),
+        v_t=torch.empty((heads, rows // 128, dim, 128), dtype=operand_dtype, device=dev),
     )
     if pool:
         prep.q_hi = torch.empty((heads, layout.q_tiles, dim), dtype=torch.bfloat16, device=dev)
@@ -135,11 +140,11 @@ def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.T
         prep.k_hi = torch.empty((heads, layout.k_tiles, dim), dtype=torch.bfloat16, device=dev)
         prep.k_lo = torch.empty_like(prep.k_hi)
     if check_overflow:
-        prep.v_overflow = torch.zeros(1, dtype=torch.int32, device=dev)
+        prep.overflow = torch.zeros(1, dtype=torch.int32, device=dev)
     _lib.call("dfs_prepare_qkv", _ptr(q), _ptr(k), _ptr(v), _ptr(perm), heads, length, dim,
-              DTYPE_CODE[q.dtype], layout.video_len, layout.tile, DTYPE_CODE[pv_dtype],
+              DTYPE_CODE[q.dtype], layout.video_len, layout.tile, DTYPE_CODE[operand_dtype],
               _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(prep.q_hi), _ptr(prep.q_lo),
-              _ptr(prep.k_hi), _ptr(prep.k_lo), _ptr(prep.v_overflow), _stream(q))
+              _ptr(prep.k_hi), _ptr(prep.k_lo), _ptr(prep.overflow), _stream(q))
     return prep
 
 
@@ -202,8 +207,8 @@ def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale:
     lse = torch.empty((prep.heads, L), dtype=torch.float32, device=out.device) if want_lse else None
     scale = 1.0 / math.sqrt(prep.head_dim) if scale is None else float(scale)
     _lib.call("dfs_bsa_fwd", _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(row_ptr),
-              _ptr(col_idx), prep.heads, L, prep.head_dim, DTYPE_CODE[prep.dtype],
-              DTYPE_CODE[prep.pv_dtype], scale, _ptr(out), DTYPE_CODE[out_dtype], _ptr(out_perm),
+              _ptr(col_idx), prep.heads, L, prep.head_dim, DTYPE_CODE[prep.operand_dtype],
+              DTYPE_CODE[prep.operand_dtype], scale, _ptr(out), DTYPE_CODE[out_dtype], _ptr(out_perm),
               _ptr(lse), _stream(prep.q_perm))
     return (out, lse) if want_lse else out
 

@@ -76,27 +76,30 @@ int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst,
 /*
  * Fused permute of Q, K, V into the attention operand layouts plus mean
  * pooling of Q and K over tile_size-token tiles in the scoring layout.
- *   dtype        0 (bf16) or 1 (f16) for q, k, v, q_perm, k_perm.
+ *   dtype        0 (bf16) or 1 (f16) for the inputs q, k, v.
  *   video_len    L for Wan; the video token count for HunyuanVideo. The
  *                scoring layout is [video | zero pad to 128 | text | zero
  *                pad to ceil(L/128)*128] (attention_hyvideo.py:331-365;
  *                for Wan, attention_wan.py:176-189).
- *   pv_dtype     0: v_t holds the bf16 bits of v; 1: v_t holds v in f16.
+ *   operand_dtype  dtype of q_perm, k_perm and v_t: 0 keeps the bf16 bits
+ *                (bf16 inputs only); 1 holds f16 (bf16 inputs are rounded
+ *                to f16, exact for values inside the f16 range).
  *   q_pool_*     [H][ceil(video_len/128)*128/tile][D] (may all be NULL to skip
  *   k_pool_*     [H][ceil(L/128)*128/tile][D]          pooling: cached steps).
- *   v_overflow   optional int32 flag, set to 1 when pv_dtype = 1 and some
- *                |v| exceeds the f16 range.
+ *                Means of the input values, whatever operand_dtype.
+ *   overflow     optional int32 flag, set to 1 when bf16 inputs are rounded
+ *                to f16 and some |q|, |k| or |v| exceeds the f16 range.
  * Replaces the q/k/v gathers of attention_wan.py:173-174, 338-340 and the
  * padding + tile means of attention_wan.py:176-205.
  */
 int dfs_prepare_qkv(const void* q, const void* k, const void* v,
                     const int32_t* perm, int64_t heads, int64_t seq_len,
                     int64_t head_dim, int dtype, int64_t video_len,
-                    int64_t tile_size, int pv_dtype,
+                    int64_t tile_size, int operand_dtype,
                     void* q_perm, void* k_perm, void* v_t,
                     uint16_t* q_pool_hi, uint16_t* q_pool_lo,
                     uint16_t* k_pool_hi, uint16_t* k_pool_lo,
-                    int32_t* v_overflow, dfs_stream_t stream);
+                    int32_t* overflow, dfs_stream_t stream);
 
 /*
  * Hierarchical block scoring and top-k in one kernel: pooled QK^T * D^-1/2
@@ -142,7 +145,11 @@ int dfs_topk_from_scores(const float* scores, int64_t heads,
 
 /*
  * Block-sparse flash-attention forward over the kept 128x128 blocks.
- *   q_perm, k_perm, v_t  as produced by dfs_prepare_qkv (dtype, pv_dtype).
+ *   q_perm, k_perm, v_t  as produced by dfs_prepare_qkv; dtype is the dtype
+ *                        of q_perm and k_perm, pv_dtype that of v_t (f16/f16
+ *                        and bf16/bf16 as prepared; bf16/f16 also accepted).
+ *                        With f16 q_perm the kernel folds scale * log2(e)
+ *                        into Q, rounding Q * scale * log2(e) to f16.
  *   scale                softmax scale (the reference passes None -> D^-1/2).
  *   out                  out_dtype 0/1/2; when out_perm is NULL, out is
  *                        [H][L][D] in execution order; otherwise row i is

@@ -76,20 +76,38 @@ def test_prepare_qkv_matches_oracle(dev, case):
     vperm = torch.randperm(video)
     perm, _ = orc.full_permutation(vperm, length)
     layout = ScoringLayout(length, video, tile)
-    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout, pv_dtype=pv,
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout, operand_dtype=pv,
                            check_overflow=True)
     qp, kp, vp = (orc.apply_permutation(x, perm) for x in (q, k, v))
     R = layout.rows
     pad = lambda x: torch.cat([x[0], x.new_zeros(heads, R - length, d)], dim=1)
-    assert torch.equal(prep.q_perm.cpu(), pad(qp))
-    assert torch.equal(prep.k_perm.cpu(), pad(kp))
+    assert prep.q_perm.dtype == pv and prep.k_perm.dtype == pv  # f16 operands: exact bf16 -> f16 rounding
+    assert torch.equal(prep.q_perm.cpu(), pad(qp).to(pv))
+    assert torch.equal(prep.k_perm.cpu(), pad(kp).to(pv))
     assert torch.equal(prep.v_t.cpu(), vt_reference(pad(vp), pv))
-    assert int(prep.v_overflow.item()) == 0
+    assert int(prep.overflow.item()) == 0
     qt, kt = orc.pooled_tiles(qp, kp, tile, 128, video)
     for hi, lo, ref in ((prep.q_hi, prep.q_lo, qt[0]), (prep.k_hi, prep.k_lo, kt[0])):
         got = hi.cpu().float() + lo.cpu().float()
         assert got.shape == ref.shape
         assert torch.allclose(got, ref, rtol=2e-5, atol=1e-6), float((got - ref).abs().max())
+
+
+def test_prepare_flags_f16_overflow(dev):
+    """bf16 inputs rounded to f16 operands: a finite value beyond the f16 range
+    (in q, k or v) raises the overflow flag; bf16 operands keep the bits."""
+    heads, length, d = 1, 300, 64
+    layout = ScoringLayout(length, length, 16)
+    ident = torch.arange(length, dtype=torch.int32, device=dev)
+    for which in range(3):
+        qkv = [torch.randn((1, heads, length, d)).to(torch.bfloat16) for _ in range(3)]
+        qkv[which][0, 0, 123, 7] = 1.0e6
+        prep = ops.prepare_qkv(*(x.to(dev) for x in qkv), ident, layout, check_overflow=True, pool=False)
+        assert int(prep.overflow.item()) == 1, which
+        keep = ops.prepare_qkv(*(x.to(dev) for x in qkv), ident, layout, operand_dtype=torch.bfloat16,
+                               check_overflow=True, pool=False)
+        assert int(keep.overflow.item()) == 0
+        assert torch.equal(keep.q_perm.cpu()[:, :length], qkv[0][0])
 
 
 def _random_scores(heads, rows, cols, seed, ties=False):
@@ -175,7 +193,7 @@ def _run_bsa(dev, q, k, v, mask_bool, pv, out_dtype, perm=None):
     heads, length, d = q.shape[1], q.shape[2], q.shape[3]
     layout = ScoringLayout(length, length, 16)
     ident = torch.arange(length, dtype=torch.int32)
-    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident.to(dev), layout, pv_dtype=pv, pool=False)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident.to(dev), layout, operand_dtype=pv, pool=False)
     row_ptr, col_idx = ops.mask_to_csr(mask_bool.to(dev))
     out = ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=out_dtype,
                       out_perm=None if perm is None else perm.to(dev, torch.int32))
@@ -273,3 +291,30 @@ def test_rows_keeping_only_a_short_tail_block(dev, monkeypatch, schedule):
     assert torch.isfinite(out).all()
     ref = orc.masked_attention(q, k, v, mask)
     assert float((out - ref).abs().max()) <= 2e-2 and mean_rel(out, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_bsa_fwd_rising_and_negative_logits(dev, monkeypatch, schedule):
+    """Logits that grow block after block (the running maximum jumps by far
+    more than the lazy-rescale threshold several times) and rows whose
+    logits are all strongly negative: the output still equals fp32 masked
+    attention."""
+    _set_schedule(monkeypatch, schedule)
+    heads, d, length = 2, 128, 1200
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn((1, heads, length, d), generator=g)
+    k = torch.randn((1, heads, length, d), generator=g)
+    v = torch.randn((1, heads, length, d), generator=g)
+    nb = math.ceil(length / 128)
+    ramp = torch.linspace(0.2, 3.0, nb).repeat_interleave(128)[:length]
+    k = k * ramp[None, None, :, None]          # later key blocks give much larger |logits|
+    q[:, 1] = -q[:, 1].abs()                   # head 1: many large negative logits
+    k[:, 1] = k[:, 1].abs()
+    q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    mask = torch.rand((heads, nb, nb), generator=g) < 0.6
+    mask[:, torch.arange(nb), torch.arange(nb)] = True
+    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32)
+    ref = orc.masked_attention(q, k, v, mask)
+    assert torch.isfinite(out).all()
+    assert float((out - ref).abs().max()) <= 2e-2 and mean_rel(out, ref) <= 1e-3, \
+        (float((out - ref).abs().max()), mean_rel(out, ref))
