@@ -17,9 +17,12 @@
 //    workgroups per CU, single K and V buffers, the K copy of the next block
 //    overlapping softmax and PV, the V copy overlapping the next QK^T; the
 //    other workgroup on the CU fills the gaps.
-//  * duo (DFSATTN_AMD_BSA_KERNEL=duo): one eight-wave workgroup per CU for
-//    two adjacent query blocks, key blocks kept by both copied once (the
-//    schedule is described at the kernel).
+//  * ping-pong (DFSATTN_AMD_BSA_KERNEL=pp, f16 operands): one eight-wave
+//    workgroup per CU for two adjacent query blocks, the two four-wave groups
+//    alternating MFMA and softmax phases half a cycle apart (described at the
+//    kernel). It overlaps VALU with MFMA work but concentrates the LDS operand
+//    reads of a CU into its MFMA phases; at the 75.6k-token shape it runs about
+//    10% slower than split.
 //
 // LDS rows are 256 bytes; 16-byte chunk c of row r is stored at chunk
 // c ^ (r % 16) so the 32 rows read by one MFMA operand fetch hit distinct
@@ -348,9 +351,10 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
 
   if (beg < end) {
     const uint32_t head_bytes = static_cast<uint32_t>(p.R) * D * 2;
-    const sgpr4 krs = make_rsrc(k + static_cast<int64_t>(h) * p.R * D, head_bytes);
-    const sgpr4 vrs = make_rsrc(vt + static_cast<int64_t>(h) * p.R * D, head_bytes);
-    const uint32_t k_base = lds_addr(k_lds), v_base = lds_addr(v_lds);
+    const auto krs = make_rsrc(k + static_cast<int64_t>(h) * p.R * D, head_bytes);
+    const auto vrs = make_rsrc(vt + static_cast<int64_t>(h) * p.R * D, head_bytes);
+    void* const k_base = k_lds;
+    void* const v_base = v_lds;
     const int ws = __builtin_amdgcn_readfirstlane(w);
     const TileCopy<D * 2> kcopy(ws, lane);
     const TileCopy<256> vcopy(ws, lane);
@@ -459,10 +463,10 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
     const bool tail_possible = (p.L & 127) != 0;
 
     for (int t = 0; t < n; ++t) {
-      // Past the last block the copies target a block beyond the buffer:
-      // out-of-range buffer loads return zero and fetch nothing, so every
-      // iteration issues the same number of loads and the waits stay fixed.
-      const int kb_next = t + 1 < n ? col_at(t + 1) : p.Kb;
+      // After the last block the copies reload the current block into the
+      // buffers it has just left (in range; nobody reads them again), so every
+      // iteration issues the same loads and the vmcnt waits stay fixed.
+      const int kb_next = t + 1 < n ? col_at(t + 1) : kb;
       wait_vmcnt<V_LOADS>();  // this wave's K copies have landed
       block_barrier();        // ... and everybody else's
       f32x16 s[4];
@@ -492,12 +496,13 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
       vcopy.template issue<V_LOADS>(vrs, kb_next * TILE_BYTES, v_base, ws);
       kb = kb_next;
     }
-    wait_vmcnt_0();  // the trailing (empty) copies have retired
+    wait_vmcnt_0();  // the trailing copies have landed before the workgroup's LDS is released
   }
   store_out<D>(p, out, out_perm, lse, o, m, lsum, h, qrow, hl);
 }
 
-// Helpers of the duo schedule below: key blocks streamed as 64-key halves.
+// (head, pair of query blocks) of an eight-wave workgroup; head-major across
+// XCDs like wg_coords.
 
 template <int G>
 __device__ __forceinline__ bool group_coords(const BsaParams& p, int& h, int& grp) {
@@ -509,147 +514,38 @@ __device__ __forceinline__ bool group_coords(const BsaParams& p, int& h, int& gr
   return grp < groups;
 }
 
-// Copy of one V^T half block: D rows of 64 keys (128 bytes) taken from the
-// 256-byte rows of the V^T block, into LDS rows of 128 bytes. 16-byte chunk
-// c of row r is stored at chunk c ^ ((r >> 1) & 7): the 16 rows read by one
-// MFMA operand fetch then cover all 16 bank groups.
-struct VHalfCopy {
-  uint32_t voff;
-  __device__ __forceinline__ VHalfCopy(int wave, int lane) {
-    const int r = wave * 8 + (lane >> 3);  // 8 rows per wave instruction
-    voff = static_cast<uint32_t>(r * 256 + (((lane & 7) ^ ((r >> 1) & 7)) * 16));
-  }
-  // LOADS loads per thread (4 * LOADS KiB) of the half starting at byte off.
-  template <int LOADS>
-  __device__ __forceinline__ void issue(sgpr4 rs, uint32_t off, uint32_t lds_base, int wave) const {
-    asm volatile("" : "+s"(lds_base));
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j)  // load j of wave w: rows (4j + w) * 8 .. +7
-      load_lds16(rs, lds_base + (j * 4 + wave) * 1024, voff, off + j * 32 * 256);
-  }
+struct BsaArgs {
+  const uint16_t *q, *k, *vt;
+  const int32_t *row_ptr, *col_idx;
+  void* out;
+  const int32_t* out_perm;
+  float* lse;
 };
 
-__device__ __forceinline__ uint4 vhalf_chunk(const uint16_t* lds, int r, int c) {
-  return *reinterpret_cast<const uint4*>(lds + (r * 8 + (c ^ ((r >> 1) & 7))) * 8);
-}
-
-// The copies of the next stage (K half + V^T half of one key block, N loads
-// per thread), issued a few at a time between the MFMAs of the current stage
-// rather than in one burst: a burst of 1 KiB loads from every wave stalls the
-// waves at the load issue before they can compute. Part i goes out at the
-// (i * 6 / N)-th of the six issue points of a half step.
-template <int D>
-struct StageCopy {
-  static constexpr int K_LOADS = D / 32, V_LOADS = D / 32, N = K_LOADS + V_LOADS;
-  sgpr4 krs, vrs;
-  uint32_t kvoff, vvoff;
-  uint32_t koff, voff;  // global byte offsets of the pending stage
-  uint32_t kdst, vdst;  // LDS byte addresses of its buffers
-  int ws;
-  __device__ __forceinline__ void set(uint32_t col_off, int half, uint32_t dst) {
-    koff = col_off + half * (128 * D);  // 64 K rows of 2D bytes
-    voff = col_off + half * 128;        // 64 keys of each 256-byte V^T row
-    kdst = dst;
-    vdst = dst + 64 * D * 2;
-    asm volatile("" : "+s"(koff), "+s"(voff), "+s"(kdst), "+s"(vdst));
-  }
-  template <int I>
-  __device__ __forceinline__ void part() const {
-    if constexpr (I < K_LOADS)
-      load_lds16(krs, kdst + (I * 4 + ws) * 1024, kvoff, koff + I * 4 * 1024);
-    else
-      load_lds16(vrs, vdst + ((I - K_LOADS) * 4 + ws) * 1024, vvoff, voff + (I - K_LOADS) * 32 * 256);
-  }
-  template <int E, int I = 0>
-  __device__ __forceinline__ void at() const {
-    if constexpr (I < N) {
-      if constexpr (I * 6 / N == E) part<I>();
-      at<E, I + 1>();
-    }
-  }
-  template <int I = 0>
-  __device__ __forceinline__ void all() const {
-    if constexpr (I < N) {
-      part<I>();
-      all<I + 1>();
-    }
-  }
-};
-
-// Per-lane LDS byte addresses of the operand rows of one half step. The
-// swizzled 16-byte chunk of an operand read is (2 * step) ^ y for a lane
-// constant y, formed at the read with one XOR-add (v_xad_u32) instead of being
-// kept in registers for every step: the two-query-block kernel has none to
-// spare.
-struct HalfAddr {
-  uint32_t k_row;  // K half: byte address of row l32 (chunk 0)
-  uint32_t ky;     // (hl ^ (l32 & 15)) << 4
-  uint32_t v_row;  // V^T half: byte address of row l32 (chunk 0)
-  uint32_t vy;     // (hl ^ ((l32 >> 1) & 7)) << 4
-};
-
-template <int D>
-__device__ __forceinline__ HalfAddr half_addr(uint32_t k_half, uint32_t v_half, int l32, int hl) {
-  HalfAddr a;
-  a.k_row = k_half + static_cast<uint32_t>(l32 * D * 2);
-  a.ky = static_cast<uint32_t>((hl ^ (l32 & (D / 8 - 1))) << 4);
-  a.v_row = v_half + static_cast<uint32_t>(l32 * 128);
-  a.vy = static_cast<uint32_t>((hl ^ ((l32 >> 1) & 7)) << 4);
-  return a;
-}
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef const __attribute__((address_space(3))) u32x4* lds_u32x4_ptr;
-
-// 16-byte LDS read at byte address addr.
-__device__ __forceinline__ uint4 lds_read16(uint32_t addr) {
-  const u32x4 v = *(lds_u32x4_ptr)(static_cast<uintptr_t>(addr));
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-// One 64-key half step for one query block: S^T in 32-key chunks of online
-// softmax (NC chunks per pass), then O^T += V^T P^T.
-template <int D, typename QkOp, typename PvOp, int NC, typename CP>
-__device__ __forceinline__ void half_step(HalfAddr ad, const typename QkOp::vec* qf, float scale_log2, float& m,
-                                          float& lsum, f32x16* o, int valid, int hl, const CP& cp) {
-  constexpr int DS = D / 16, DCH = D / 32;
-  // Fresh each step: keeps the per-step addresses out of the loop-carried
-  // register set.
-  asm volatile("" : "+v"(ad.k_row), "+v"(ad.ky), "+v"(ad.v_row), "+v"(ad.vy));
+// Softmax of one block for the ping-pong schedule, in two halves. S (log2
+// units, from the prescaled Q) arrives without the running reference; the
+// first half takes the block maximum, moves the reference m lazily (when a
+// row's maximum exceeds m + kLazyTau, or on the row's first block) rescaling
+// O and l, and forms P = exp2(S - m) for keys 0-63; the second half forms P
+// for keys 64-127. P (f16, the PV operand order) stays in registers until the
+// next MFMA phase. The VALU work of this phase overlaps the other group's
+// MFMAs, so the subtraction costs little and saves the 16 registers a C
+// input would hold.
+template <int DCH>
+__device__ __forceinline__ void pp_softmax_first(const f32x16* s, bool first, float& m, float& lsum, f32x16* o,
+                                                 f16x8* pf) {
+  typedef MfmaOp<true> Op;
+  float mx = -INFINITY;
 #pragma unroll
-  for (int c0 = 0; c0 < 2; c0 += NC) {
-    f32x16 s[NC];
+  for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
-    for (int kc = 0; kc < NC; ++kc) {
-      s[kc] = f32x16{};
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        const uint4 a = lds_read16((((2u * ds) << 4) ^ ad.ky) + ad.k_row + (c0 + kc) * 32 * D * 2);
-        s[kc] = QkOp::run(__builtin_bit_cast(typename QkOp::vec, a), qf[ds], s[kc]);
-      }
-      // Issue points: QK chunk ends, then PV step ends, in program order.
-      if constexpr (NC == 2) {
-        if (kc == 0) cp.template at<0>(); else cp.template at<1>();
-      } else {
-        if (c0 == 0) cp.template at<0>(); else cp.template at<3>();
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (valid < 64) {  // keys >= valid of this half are past L
-#pragma unroll
-      for (int kc = 0; kc < NC; ++kc)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if ((c0 + kc) * 32 + (r >> 2) * 8 + hl * 4 + (r & 3) >= valid) s[kc][r] = -INFINITY;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kc = 0; kc < NC; ++kc)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kc][r]);
-    const float mnew = fmaxf(m, xhalf_max(mx) * scale_log2);
-    if (__any(mnew > m)) {
-      const float alpha = exp2_fast(m - mnew);  // 0 for an empty state (m = -inf, mnew finite)
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kc][r]);
+  const float bm = xhalf_max(mx);
+  if (first || __any(bm > m + kLazyTau)) {
+    float mnew = first ? bm : fmaxf(bm, m);
+    if (!(mnew > -INFINITY)) mnew = m;  // a row with every key masked keeps m
+    if (!first) {
+      const float alpha = exp2_fast(m - mnew);
       lsum *= alpha;
 #pragma unroll
       for (int i = 0; i < DCH; ++i)
@@ -657,76 +553,116 @@ __device__ __forceinline__ void half_step(HalfAddr ad, const typename QkOp::vec*
         for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
     }
     m = mnew;
-    // A fully masked chunk seen before any key: exponentiate against 0 so
-    // P = exp2(-inf) = 0, not NaN.
-    const float mref = mnew == -INFINITY ? 0.f : mnew;
+  }
 #pragma unroll
-    for (int ks = 0; ks < 2 * NC; ++ks) {
-      const f32x16& src = s[ks >> 1];
-      const int r0 = (ks & 1) * 8;
-      typename PvOp::pair pr[4];
+  for (int ks = 0; ks < 4; ++ks) {
+    Op::pair pr[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pr[j] = PvOp::pack(exp2_fast(fmaf(src[r0 + 2 * j], scale_log2, -mref)),
-                           exp2_fast(fmaf(src[r0 + 2 * j + 1], scale_log2, -mref)));
-        lsum = PvOp::sum2(pr[j], lsum);
-      }
-      const typename PvOp::vec pf = __builtin_bit_cast(typename PvOp::vec, pr);
-      const uint32_t vcol = ((2u * (c0 * 2 + ks)) << 4) ^ ad.vy;
-#pragma unroll
-      for (int dc = 0; dc < DCH; ++dc) {
-        const uint4 a = lds_read16(vcol + ad.v_row + dc * 32 * 128);
-        o[dc] = PvOp::run(__builtin_bit_cast(typename PvOp::vec, a), pf, o[dc]);
-      }
-      if constexpr (NC == 2) {
-        if (ks == 0) cp.template at<2>();
-        else if (ks == 1) cp.template at<3>();
-        else if (ks == 2) cp.template at<4>();
-        else cp.template at<5>();
-      } else {
-        if (c0 == 0) { if (ks == 0) cp.template at<1>(); else cp.template at<2>(); }
-        else { if (ks == 0) cp.template at<4>(); else cp.template at<5>(); }
-      }
+    for (int j = 0; j < 4; ++j) {
+      pr[j] = Op::pack(exp2_fast(s[ks >> 1][(ks & 1) * 8 + 2 * j] - m),
+                       exp2_fast(s[ks >> 1][(ks & 1) * 8 + 2 * j + 1] - m));
+      lsum = Op::sum2(pr[j], lsum);
     }
+    pf[ks] = __builtin_bit_cast(f16x8, pr);
   }
 }
 
-// Duo schedule: one workgroup of eight waves per CU serves two adjacent query
-// blocks A and B; waves 0-3 own A's 32-row groups, waves 4-7 B's. The
-// columns kept by both are shared slots (one key block, read by both
-// groups); the columns kept by only one of them are paired up, one of A's
-// with one of B's, into slots carrying two key blocks. Every wave works in
-// every slot (except the few unpaired ones), each on one query block, so the
-// per-wave registers stay those of a single query block while the bytes
-// copied are those of the union of the two rows. Slots are streamed as
-// 64-key halves through double buffers; a stage holds region A (K and V^T
-// halves of A's block) and region B (B's block, unused for shared slots).
-template <int D, bool QK_F16, bool PV_F16>
-__global__ void __launch_bounds__(512, 1) bsa_fwd_duo_kernel(BSA_KERNEL_ARGS) {
+__device__ __forceinline__ void pp_softmax_second(const f32x16* s, float m, float& lsum, f16x8* pf) {
+  typedef MfmaOp<true> Op;
+#pragma unroll
+  for (int ks = 4; ks < 8; ++ks) {
+    Op::pair pr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pr[j] = Op::pack(exp2_fast(s[ks >> 1][(ks & 1) * 8 + 2 * j] - m),
+                       exp2_fast(s[ks >> 1][(ks & 1) * 8 + 2 * j + 1] - m));
+      lsum = Op::sum2(pr[j], lsum);
+    }
+    pf[ks] = __builtin_bit_cast(f16x8, pr);
+  }
+}
+
+// Scheduling of an MFMA phase: the LDS operand reads run kAhead MFMAs ahead
+// of their MFMAs, so each read's latency is covered by the MFMAs before its
+// use (in the ping-pong schedule the other wave on the SIMD is doing VALU
+// work and cannot fill MFMA gaps). Pinned with scheduling-group barriers:
+// kAhead reads, then alternately one MFMA and one read, then the last MFMAs.
+constexpr int kAhead = 4;
+template <int N>
+__device__ __forceinline__ void pin_read_ahead_schedule() {
+  constexpr int kMfma = 0x008, kDsRead = 0x100;
+  __builtin_amdgcn_sched_group_barrier(kDsRead, kAhead, 0);
+#pragma unroll
+  for (int i = 0; i < N - kAhead; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(kMfma, kAhead, 0);
+}
+
+// O^T += V^T P^T from an LDS V^T tile and P held in registers.
+template <int D>
+__device__ __forceinline__ void pv_tile_regs(const uint16_t* v_tile, const f16x8* pf, f32x16* o, int l32, int hl) {
+  constexpr int DCH = D / 32, N = 8 * DCH;
+  uint4 a[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) a[i] = lds_chunk<16>(v_tile, (i % DCH) * 32 + l32, (i / DCH) * 2 + hl);
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    o[i % DCH] = MfmaOp<true>::run(__builtin_bit_cast(f16x8, a[i]), pf[i / DCH], o[i % DCH]);
+  pin_read_ahead_schedule<N>();
+}
+
+// S^T = K Q^T from an LDS K tile, with the read-ahead schedule above.
+template <int D>
+__device__ __forceinline__ void qk_tile_ahead(const uint16_t* k_tile, const f16x8* qf, int l32, int hl, f32x16* s) {
+  constexpr int CPR = D / 8, DS = D / 16, N = 4 * DS;
+  uint4 a[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) a[i] = lds_chunk<CPR>(k_tile, (i / DS) * 32 + l32, (i % DS) * 2 + hl);
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc) s[kc] = f32x16{};
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    s[i / DS] = MfmaOp<true>::run(__builtin_bit_cast(f16x8, a[i]), qf[i % DS], s[i / DS]);
+  pin_read_ahead_schedule<N>();
+}
+
+// Ping-pong schedule (f16 operands). One workgroup of eight
+// waves per CU serves two adjacent query blocks of a head: waves 0-3 (group
+// 0) run block 2i, waves 4-7 (group 1) block 2i+1, each group with its own K
+// and V buffers and its own column list (the columns both rows keep first, in
+// the same order, so the second fetch of a shared key block hits L2). Each
+// group alternates an MFMA phase (PV of block k-1, then QK^T of block k) with
+// a VALU phase (softmax of block k), and the groups run half a cycle apart:
+// every SIMD holds one wave of each group, so one wave's exponentials issue
+// while the other's MFMAs run. Every phase has two workgroup barriers (mid,
+// end), the same number for all waves, which keeps the groups in step.
+// Copies: V(k) is issued at the mid barrier of MFMA phase k (after PV(k-1)
+// left the V buffer) and K(k+1) at the start of VALU phase k (after QK^T(k)
+// left the K buffer); each lands at least one and a half phases before use.
+// A group past its last block issues no copies and keeps taking part in the
+// barriers until the other group is done.
+template <int D>
+__global__ void __launch_bounds__(512, 1) bsa_fwd_pp_kernel(BSA_KERNEL_ARGS) {
+  constexpr int DCH = D / 32;
+  constexpr int LOADS = D / 16;  // 16-byte loads per thread for one tile (4 waves)
   constexpr uint32_t TILE_BYTES = 128 * D * 2;
-  constexpr int HALF = 64 * D;                   // uint16 elements of a K (or V^T) half
-  constexpr int REGION = 2 * HALF;               // K half + V^T half
-  constexpr int STAGE = 2 * REGION;              // regions A and B
-  constexpr uint16_t NONE = 0xFFFF;
-  typedef MfmaOp<QK_F16> QkOp;
-  typedef MfmaOp<PV_F16> PvOp;
-  __shared__ __attribute__((aligned(16))) uint16_t tiles[2 * STAGE];
-  __shared__ int n_slots;
-  // Dynamic LDS: bitmaps of A and B (W words each), then the slot columns
-  // col_a[Kb], col_b[Kb] (uint16, NONE when the slot has no block there).
-  extern __shared__ uint32_t dyn[];
+  constexpr uint16_t NONE = 0xFFFFu;
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][128 * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * 128];
+  __shared__ int n_rows[2];
+  extern __shared__ uint32_t dyn[];  // bitmaps [2][W], then columns [2][Kb] (uint16)
 
   int h, grp;
   if (!group_coords<2>(p, h, grp)) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int g = __builtin_amdgcn_readfirstlane(w >> 2), rg = w & 3;  // wave-uniform
+  const int g = __builtin_amdgcn_readfirstlane(w >> 2), rg = __builtin_amdgcn_readfirstlane(w & 3);
   const int W = (p.Kb + 31) >> 5;
-  uint32_t* bm = dyn;  // [2][W]
-  uint16_t* col_a = reinterpret_cast<uint16_t*>(dyn + 2 * W);
-  uint16_t* col_b = col_a + p.Kb;
+  uint32_t* bm = dyn;
+  uint16_t* cols = reinterpret_cast<uint16_t*>(dyn + 2 * W);  // [2][Kb]
 
   for (int i = tid; i < 2 * W; i += 512) bm[i] = 0u;
-  for (int i = tid; i < 2 * p.Kb; i += 512) col_a[i] = NONE;
   block_barrier();
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
@@ -734,19 +670,17 @@ __global__ void __launch_bounds__(512, 1) bsa_fwd_duo_kernel(BSA_KERNEL_ARGS) {
     if (qr < p.Qb) {
       const int64_t row = static_cast<int64_t>(h) * p.Qb + qr;
       const int beg = row_ptr[row];
-      const int n = min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
-      for (int i = tid; i < n; i += 512) {
+      const int cnt = min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
+      for (int i = tid; i < cnt; i += 512) {
         const int c = col_idx[beg + i];
-        if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb))
-          atomicOr(&bm[r * W + (c >> 5)], 1u << (c & 31));
+        if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) atomicOr(&bm[r * W + (c >> 5)], 1u << (c & 31));
       }
     }
   }
   block_barrier();
   if (w == 0) {
-    // Shared columns fill slots 0.. in ascending order; A-only columns fill
-    // col_a and B-only columns col_b of the slots after them, each ascending.
-    const int per = (W + 63) >> 6;  // words per lane
+    // Row r's list: the shared columns ascending, then its own ascending.
+    const int per = (W + 63) >> 6;
     const int w0 = lane * per;
     int cs = 0, ca = 0, cb = 0;
     for (int j = 0; j < per && w0 + j < W; ++j) {
@@ -771,125 +705,127 @@ __global__ void __launch_bounds__(512, 1) bsa_fwd_duo_kernel(BSA_KERNEL_ARGS) {
       const uint32_t a = bm[w0 + j], b = bm[W + w0 + j];
       uint32_t x = a & b;
       while (x) {
-        const int c = (w0 + j) * 32 + __ffs(x) - 1;
+        const uint16_t c = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
         x &= x - 1;
-        col_a[ps] = static_cast<uint16_t>(c);
-        col_b[ps] = static_cast<uint16_t>(c);
+        cols[ps] = c;
+        cols[p.Kb + ps] = c;
         ++ps;
       }
       x = a & ~b;
       while (x) {
-        col_a[pa++] = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
+        cols[pa++] = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
         x &= x - 1;
       }
       x = b & ~a;
       while (x) {
-        col_b[pb++] = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
+        cols[p.Kb + pb++] = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
         x &= x - 1;
       }
     }
-    if (lane == 63) n_slots = n_shared + max(ia, ib);
+    if (lane == 63) {
+      n_rows[0] = n_shared + ia;
+      n_rows[1] = n_shared + ib;
+    }
   }
+  block_barrier();
+  const int qb = grp * 2 + g;
+  const int n = qb < p.Qb ? n_rows[g] : 0;
+  const int n_all = max(grp * 2 < p.Qb ? n_rows[0] : 0, grp * 2 + 1 < p.Qb ? n_rows[1] : 0);
+  const uint16_t* my_cols = cols + g * p.Kb;
+  (void)NONE;
 
-  constexpr int DCH = D / 32;
   f32x16 o[DCH];
 #pragma unroll
   for (int i = 0; i < DCH; ++i) o[i] = f32x16{};
-  float m = -INFINITY, lsum = 0.f;
-  typename QkOp::vec qf[D / 16];
-  const int qb = grp * 2 + g;
+  float m = 0.f, lsum = 0.f;
+  f16x8 qf[D / 16];
   const int qrow = qb * 128 + rg * 32 + l32;
-  if (qb < p.Qb) {
-    load_q<D, QkOp>(q, p, h, qrow, hl, qf);
-#pragma unroll
-    for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qf[s]));
-  }
-  block_barrier();
-  const int T = __builtin_amdgcn_readfirstlane(n_slots);
+  if (n > 0) load_q_scaled<D>(q, p, h, qrow, hl, qf);
 
-  if (T > 0) {
-    const uint32_t head_bytes = static_cast<uint32_t>(p.R) * D * 2;
-    const sgpr4 krs = make_rsrc(k + static_cast<int64_t>(h) * p.R * D, head_bytes);
-    const sgpr4 vrs = make_rsrc(vt + static_cast<int64_t>(h) * p.R * D, head_bytes);
-    const uint32_t base = lds_addr(tiles);
-    const int ws = __builtin_amdgcn_readfirstlane(rg);  // wave index within its group
-    StageCopy<D> cp;
-    cp.krs = krs;
-    cp.vrs = vrs;
-    cp.kvoff = TileCopy<D * 2>(ws, lane).voff;
-    cp.vvoff = VHalfCopy(ws, lane).voff;
-    cp.ws = ws;
-    const bool tail_possible = (p.L & 127) != 0;
-    // Group 0 copies slot blocks into region A, group 1 into region B; a
-    // region with nothing to hold copies the out-of-range block Kb (zeros,
-    // nothing fetched) so every wave issues the same loads every stage.
-    auto copy_col = [&](int t) -> int {
-      if (t >= T) return p.Kb;
-      const int a = __builtin_amdgcn_readfirstlane(static_cast<int>(col_a[t]));
-      if (g == 0) return a == NONE ? p.Kb : a;
-      const int b = __builtin_amdgcn_readfirstlane(static_cast<int>(col_b[t]));
-      return (b == NONE || b == a) ? p.Kb : b;
-    };
-    auto stage_dst = [&](int half) { return base + static_cast<uint32_t>((half * STAGE + g * REGION) * 2); };
-    int cc = copy_col(0);
-    cp.set(static_cast<uint32_t>(cc) * TILE_BYTES, 0, stage_dst(0));
-    cp.all();
-    for (int t = 0; t < T; ++t) {
-      const int cn = copy_col(t + 1);
-      const int a = __builtin_amdgcn_readfirstlane(static_cast<int>(col_a[t]));
-      const int b = __builtin_amdgcn_readfirstlane(static_cast<int>(col_b[t]));
-      const int mine = g == 0 ? a : b;                 // this group's block in slot t
-      const int reg = (g == 1 && b != a) ? 1 : 0;      // region holding it
-      int valid = 128;
-      if (tail_possible && mine == p.Kb - 1) valid = p.L - mine * 128;
+  const uint32_t head_bytes = static_cast<uint32_t>(p.R) * D * 2;
+  const auto krs = make_rsrc(k + static_cast<int64_t>(h) * p.R * D, head_bytes);
+  const auto vrs = make_rsrc(vt + static_cast<int64_t>(h) * p.R * D, head_bytes);
+  void* const k_base = k_lds[g];
+  void* const v_base = v_lds[g];
+  const TileCopy<D * 2> kcopy(rg, lane);
+  const TileCopy<256> vcopy(rg, lane);
+  auto col_at = [&](int t) -> int { return t < n ? __builtin_amdgcn_readfirstlane(my_cols[t]) : p.Kb; };
+  const bool tail_possible = (p.L & 127) != 0;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        wait_vmcnt_0();   // this wave's copies of this stage have landed
-        block_barrier();  // everybody's, and the previous stage is no longer read
-        // The next stage: the other half of this slot, or half 0 of the next.
-        if (half == 0)
-          cp.set(static_cast<uint32_t>(cc) * TILE_BYTES, 1, stage_dst(1));
-        else
-          cp.set(static_cast<uint32_t>(cn) * TILE_BYTES, 0, stage_dst(0));
-        if (mine != NONE) {
-          const uint32_t rb = base + static_cast<uint32_t>((half * STAGE + reg * REGION) * 2);
-          const HalfAddr ad = half_addr<D>(rb, rb + HALF * 2, l32, hl);
-          half_step<D, QkOp, PvOp, 2>(ad, qf, p.scale_log2, m, lsum, o, valid - half * 64, hl, cp);
-        } else {
-          cp.all();
-        }
-      }
-      cc = cn;
+  for (int s2 = 0; s2 < D / 16; ++s2) asm volatile("" ::"v"(qf[s2]));
+
+  if (g == 0 && n > 0) kcopy.template issue<LOADS>(krs, col_at(0) * TILE_BYTES, k_base, rg);  // group 1: in V(-1)
+  f32x16 s[4];
+  f16x8 pf[8];
+  // MFMA phase kk: PV(kk-1) from the P registers, then QK^T(kk) into s.
+  auto mfma_phase = [&](int kk) {
+    if (kk >= 1 && kk - 1 < n) {
+      __builtin_amdgcn_s_setprio(1);
+      pv_tile_regs<D>(v_lds[g], pf, o, l32, hl);
+      __builtin_amdgcn_s_setprio(0);
     }
-    wait_vmcnt_0();  // the trailing (empty) copies have retired
+    wait_vmcnt_0();  // K(kk) landed
+    block_barrier();
+    const int kb = col_at(kk);
+    if (kk < n) vcopy.template issue<LOADS>(vrs, kb * TILE_BYTES, v_base, rg);
+    if (kk < n) {
+      __builtin_amdgcn_s_setprio(1);
+      qk_tile_ahead<D>(k_lds[g], qf, l32, hl, s);
+      __builtin_amdgcn_s_setprio(0);
+      if (tail_possible && kb == p.Kb - 1) {
+        int valid = p.L - kb * 128;
+        asm volatile("" : "+s"(valid));  // compares stay in this (rare) branch
+        mask_tail(s, valid, hl);
+      }
+    }
+    block_barrier();
+  };
+  // VALU phase kk: softmax of block kk into the P registers.
+  auto valu_phase = [&](int kk) {
+    const bool more = kk + 1 < n;
+    if (more) kcopy.template issue<LOADS>(krs, col_at(kk + 1) * TILE_BYTES, k_base, rg);
+    if (kk >= 0 && kk < n) pp_softmax_first<DCH>(s, kk == 0, m, lsum, o, pf);
+    block_barrier();
+    if (kk >= 0 && kk < n) pp_softmax_second(s, m, lsum, pf);
+    // V(kk) landed; K(kk+1), issued after it, may still be in flight (loads
+    // complete in issue order). Without a K copy behind it, wait for all.
+    if (more) wait_vmcnt<LOADS>(); else wait_vmcnt_0();
+    block_barrier();
+  };
+  // Group 0 runs M(i) V(i), group 1 V(i-1) M(i): the same four barriers per
+  // iteration, half a cycle apart. Group 1's V(-1) only waits.
+  if (g == 0) {
+    for (int i = 0; i <= n_all; ++i) {
+      mfma_phase(i);
+      valu_phase(i);
+    }
+  } else {
+    for (int i = 0; i <= n_all; ++i) {
+      valu_phase(i - 1);
+      mfma_phase(i);
+    }
   }
   if (qb < p.Qb) store_out<D>(p, out, out_perm, lse, o, m, lsum, h, qrow, hl);
 }
 
-struct BsaArgs {
-  const uint16_t *q, *k, *vt;
-  const int32_t *row_ptr, *col_idx;
-  void* out;
-  const int32_t* out_perm;
-  float* lse;
-};
+enum BsaSchedule { kSplit = 0, kPingPong = 1 };
 
-enum BsaSchedule { kSplit = 0, kDuo = 1 };
-
-template <int D, bool QK_F16, bool PV_F16>
-void launch_duo(const BsaArgs& a, const BsaParams& p, hipStream_t s) {
+template <int D>
+void launch_pp(const BsaArgs& a, const BsaParams& p, hipStream_t s) {
   const int groups = (p.Qb + 1) / 2, S = (groups + 7) / 8;
   const int W = (p.Kb + 31) / 32;
-  const size_t smem = static_cast<size_t>(2 * W) * sizeof(uint32_t) + static_cast<size_t>(p.Kb) * 4;
-  bsa_fwd_duo_kernel<D, QK_F16, PV_F16><<<dim3(static_cast<unsigned>(8 * S * p.H)), 512, smem, s>>>(
+  const size_t smem = static_cast<size_t>(2 * W) * sizeof(uint32_t) + static_cast<size_t>(2 * p.Kb) * 2;
+  bsa_fwd_pp_kernel<D><<<dim3(static_cast<unsigned>(8 * S * p.H)), 512, smem, s>>>(
       a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out, a.out_perm, a.lse, p);
 }
 
 template <int D, bool QK_F16, bool PV_F16>
 void launch_typed(const BsaArgs& a, const BsaParams& p, BsaSchedule sched, hipStream_t s) {
-  // The duo schedule keeps two slot column lists in LDS beside 128 KB of
-  // tiles; beyond 4096 key blocks the split schedule runs instead.
-  if (sched == kDuo && p.Kb <= 4096) return launch_duo<D, QK_F16, PV_F16>(a, p, s);
+  // The ping-pong schedule needs f16 operands and keeps 4 tiles (128 KB at
+  // D = 128) plus two uint16 column lists in LDS: it runs up to 4096 key
+  // blocks; beyond, and for bf16 operands, the split schedule runs.
+  if constexpr (QK_F16 && PV_F16)
+    if (sched == kPingPong && p.Kb <= 4096) return launch_pp<D>(a, p, s);
   const int S = (p.Qb + 7) / 8;
   dim3 grid(static_cast<unsigned>(p.sched == 0 ? 8 * S * p.H : p.H * p.Qb));
   const size_t smem = static_cast<size_t>(p.Kb) * sizeof(int32_t) +
@@ -953,9 +889,10 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   p.pair_order = (po && strcmp(po, "rotate") == 0) ? 0 : 1;
   const char* rot = getenv("DFSATTN_AMD_BSA_ROTATE");
   p.rotate = (rot && rot[0] == '0') ? 0 : 1;
-  // DFSATTN_AMD_BSA_KERNEL: "split" (default) or "duo".
   const char* kern = getenv("DFSATTN_AMD_BSA_KERNEL");
-  const BsaSchedule sched = (kern && strcmp(kern, "duo") == 0) ? kDuo : kSplit;
+  // DFSATTN_AMD_BSA_KERNEL: "split" (default) or "pp" (ping-pong, f16
+  // operands; split otherwise).
+  const BsaSchedule sched = (kern && strcmp(kern, "pp") == 0) ? kPingPong : kSplit;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool qk_f16 = dtype == DFS_DTYPE_F16, pv_f16 = pv_dtype == DFS_DTYPE_F16;
   if (head_dim == 128)

@@ -16,42 +16,23 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-typedef int32_t sgpr4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer descriptor over `bytes` bytes starting at `base` (stride 0);
-// loads past the end return zero instead of faulting.
-__device__ __forceinline__ sgpr4 make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  sgpr4 r;
-  r.x = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(a & 0xffffffffu));
-  r.y = __builtin_amdgcn_readfirstlane(static_cast<int32_t>((a >> 32) & 0xffffu));
-  r.z = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(bytes));
-  r.w = 0x00020000;
-  return r;
+// Raw buffer resource over `bytes` bytes starting at `base` (stride 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
-}
+typedef __attribute__((address_space(3))) void lds_void;
 
-// 16 bytes per lane from buffer offset voff + soff into LDS at m0 + 16 * lane.
-// Issued as inline assembly so the compiler does not serialise every later LDS
-// read behind it; the kernels wait for these loads with explicit vmcnt counts
-// (the compiler's own vmcnt waits stay correct, only more conservative). The
-// asm is volatile, so it keeps its place relative to the barrier asm (which
-// carries the memory clobber that orders the LDS reads).
-__device__ __forceinline__ void load_lds16(sgpr4 rs, uint32_t lds, uint32_t voff, uint32_t soff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
-               :
-               : "v"(voff), "s"(rs), "s"(soff), "{m0}"(lds));
-}
-
-// Copy of one tile into LDS with the chunk swizzle by NW waves: load j of wave
-// w fills LDS bytes [(NW*j + w) * 1024, +1024), i.e. 1024/ROWB rows. The
-// swizzle depends on the row modulo the chunks per row, which is the same for
-// every j, so one per-thread byte offset serves all loads and the j-th load
-// only adds j * NW KiB to the scalar offset.
+// Copy of one tile into LDS with the chunk swizzle by NW waves, as 16-byte
+// buffer loads that write LDS directly (no VGPR round trip): load j of wave w
+// reads buffer bytes tile_off + j * NW KiB + voff and fills LDS bytes
+// [(NW*j + w) * 1024, +1024) of the tile, i.e. 1024/ROWB rows. The swizzle
+// depends on the row modulo the chunks per row, which is the same for every
+// j, so one per-thread byte offset serves all loads. The loads go through the
+// compiler's buffer-to-LDS builtin, so M0, the hazards around it and the
+// waits before later reads of the same LDS object are the compiler's; the
+// kernels add explicit vmcnt waits plus a barrier before other waves read
+// the tile.
 template <int ROWB, int NW = 4>
 struct TileCopy {
   static constexpr int CPR = ROWB / 16;   // 16-byte chunks per row
@@ -61,16 +42,15 @@ struct TileCopy {
     const int r = wave * RPI + lane / CPR;
     voff = static_cast<uint32_t>(r * ROWB + (((lane % CPR) ^ (r % CPR)) * 16));
   }
-  // LOADS 16-byte loads per thread (NW * LOADS KiB in all) from byte tile_off.
+  // LOADS 16-byte loads per thread (NW * LOADS KiB in all) from byte tile_off
+  // into the LDS tile at `tile`.
   template <int LOADS>
-  __device__ __forceinline__ void issue(sgpr4 rs, uint32_t tile_off, uint32_t lds_base,
-                                        int wave) const {
-    // Opaque per call: keeps the compiler from hoisting all LOADS LDS
-    // addresses out of the loop into (spilled) scalar registers.
-    asm volatile("" : "+s"(lds_base));
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, uint32_t tile_off, void* tile, int wave) const {
 #pragma unroll
     for (int j = 0; j < LOADS; ++j)
-      load_lds16(rs, lds_base + (j * NW + wave) * 1024, voff, tile_off + j * NW * 1024);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (lds_void*)(static_cast<char*>(tile) + (j * NW + wave) * 1024), 16, voff,
+          static_cast<int>(tile_off + j * NW * 1024), 0, 0);
   }
 };
 

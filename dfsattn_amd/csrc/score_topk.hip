@@ -324,19 +324,18 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     const bool wave_scores = qbw < score_rows;
     const int nchunks = (p.k_tiles + ROWS - 1) / ROWS;
     const uint32_t head_bytes = static_cast<uint32_t>(p.k_tiles) * D * 2;
-    const sgpr4 hrs = make_rsrc(p.k_hi + static_cast<int64_t>(h) * p.k_tiles * CPR, head_bytes);
-    const sgpr4 lrs = make_rsrc(p.k_lo + static_cast<int64_t>(h) * p.k_tiles * CPR, head_bytes);
+    const auto hrs = make_rsrc(p.k_hi + static_cast<int64_t>(h) * p.k_tiles * CPR, head_bytes);
+    const auto lrs = make_rsrc(p.k_lo + static_cast<int64_t>(h) * p.k_tiles * CPR, head_bytes);
     const int ws = __builtin_amdgcn_readfirstlane(w);
     const TileCopy<D * 2> copy(ws, lane);
-    const uint32_t base = lds_addr(&kbuf[0][0][0]);
     constexpr uint32_t CHUNK_BYTES = ROWS * D * 2;
     auto issue = [&](int step) {
-      // Past the last step the copy targets the key tiles past the end: they
-      // return zero and fetch nothing, so the wait count stays fixed.
-      const int c = step < 2 * nchunks ? (step < nchunks ? step : step - nchunks) : nchunks;
-      const uint32_t dst = base + static_cast<uint32_t>((step & 1) * 2 * TILE * 2);
-      copy.template issue<LOADS>(hrs, c * CHUNK_BYTES, dst, ws);
-      copy.template issue<LOADS>(lrs, c * CHUNK_BYTES, dst + TILE * 2, ws);
+      // Past the last step the copy reloads chunk 0 into the buffer nobody
+      // reads any more, so the wait count stays fixed and every load stays in
+      // range.
+      const int c = step < 2 * nchunks ? (step < nchunks ? step : step - nchunks) : 0;
+      copy.template issue<LOADS>(hrs, c * CHUNK_BYTES, &kbuf[step & 1][0][0], ws);
+      copy.template issue<LOADS>(lrs, c * CHUNK_BYTES, &kbuf[step & 1][1][0], ws);
     };
     auto chunk_scores = [&](int buf) {
       const uint16_t* kh = &kbuf[buf][0][0];

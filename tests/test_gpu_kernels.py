@@ -200,7 +200,7 @@ def _run_bsa(dev, q, k, v, mask_bool, pv, out_dtype, perm=None):
     return out.cpu()
 
 
-SCHEDULES = ("split", "split+rotate", "duo")
+SCHEDULES = ("pp", "split", "split+rotate")
 
 
 def _set_schedule(monkeypatch, schedule):
