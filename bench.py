@@ -18,6 +18,10 @@ Q, K drifting by N(0, 0.02) per step, 12 dense warm-up steps, a mask refresh
 every 12 steps, sparsity in {0.1, 0.2, 0.3, 0.5}, sparsity_dcrt 0 and 0.1);
 each prints its own JSON line. The default run (cfg1) is the benchmark line.
 
+``--workload cfg4`` times a whole denoising step of a random-init 40-block
+Wan-style DiT with DFS self-attention against the same step with
+dense self-attention.
+
 ``--copy-calibration`` instead runs one plain 1 GiB device copy (torch's copy
 kernel), the known-size reference the FETCH_SIZE / WRITE_SIZE counters of the
 attention kernel are scaled by. The per-launch HBM traffic those counter runs
@@ -254,6 +258,66 @@ def run_cfg3(args):
             "sweep": runs}
 
 
+def run_cfg4(args):
+    """Full random-init DiT denoising step: 40 Wan-sized blocks
+    at 21x45x80 tokens with a 512-token text context, classifier-free
+    guidance (conditional + unconditional pass, as the reference's Wan
+    pipeline runs a step). The DFS step is a mask-refresh step (real step
+    12: the conditional pass selects fresh masks, the unconditional pass
+    reuses them); the dense step runs every self-attention with all blocks
+    kept (real step 0)."""
+    from dfsattn_amd import dit
+    from dfsattn_amd.attention_wan import DFS_Attention, _dfs_attention_instances
+    from dfsattn_amd.utils.order import hilbert3d_perm
+
+    cfg = dit.DIT_CONFIGS["cfg4"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"building {cfg.name}: {cfg.params() / 1e9:.2f} B parameters, random init on the GPU")
+    model = dit.build_model(cfg, dev)
+    latent, ctx, neg = dit.synth_inputs(cfg, dev)
+    timestep = torch.tensor([500.0], device=dev)
+    procs = dit.install_dfs_processors(model, "dfs", 0.3, 16, 128, hilbert3d_perm(*cfg.grid), skip_steps=12,
+                                       cache_interval=12, sparsity_dcrt=0.0)
+    torch.cuda.synchronize()
+    log("model ready")
+
+    def timed(step_idx, label):
+        for i in range(args.warmup):
+            dit.set_step(procs, step_idx)
+            dit.denoise_step(model, latent, timestep, ctx, neg)
+            torch.cuda.synchronize()
+            log(f"{label} warmup step {i + 1}/{args.warmup} done")
+        e0, e1 = _events()
+        e0.record()
+        for i in range(args.steps):
+            dit.set_step(procs, step_idx)
+            out = dit.denoise_step(model, latent, timestep, ctx, neg)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        if not bool(torch.isfinite(out).all()):
+            raise RuntimeError(f"{label} step produced non-finite values")
+        log(f"{label} step: {ms:.1f} ms")
+        return ms
+
+    sparse_ms = timed(24, "DFS (s=0.3, refresh)")
+    dense_ms = timed(0, "dense")
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()
+    return {"metric": "DiT denoising step ms (40 blocks, 75.6k tok, d5120, CFG) with DFS self-attention s=0.3",
+            "value": round(sparse_ms, 1), "unit": "ms/step", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(sparse_ms, 1), "higher_is_better": False,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (random-init N(0, 0.02) bf16 weights, N(0, 1) latent and text context; seeded)",
+            "config": {"workload": "cfg4 Wan-style DiT step: 40 blocks, hidden 5120, 40 heads, FFN 13824, "
+                                   "QK-RMSNorm + 3D RoPE, 512x4096 text context, latent 21x45x80 tokens, "
+                                   "conditional + unconditional pass, DFS refresh step (fresh masks)",
+                       "global_batch": 1, "seq_len": cfg.seq_len, "parallelism": "none (1 GPU)"},
+            "dense_step_ms": round(dense_ms, 1), "speedup_vs_dense": round(dense_ms / sparse_ms, 3),
+            "params": cfg.params()}
+
+
 def cpu_baseline(q, k, v):
     """fp32 oracle on the host cores, on the GPU run's own inputs (bf16 values
     in fp32): Hilbert permutation + pooled scoring + top-k of all 40 heads, and
@@ -332,12 +396,16 @@ def _cpu_model():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 20; 2 for cfg4)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 5; 1 for cfg4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--workload", choices=("cfg1", "cfg2", "cfg3"), default="cfg1")
+    ap.add_argument("--workload", choices=("cfg1", "cfg2", "cfg3", "cfg4"), default="cfg1")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 2 if args.workload == "cfg4" else 20
+    if args.warmup is None:
+        args.warmup = 1 if args.workload == "cfg4" else 5
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the DFS hot path is benchmarked on a single MI355X "
               "(multi-GPU sharding by head is a design note, not part of this build).", file=sys.stderr)
@@ -346,7 +414,7 @@ def main():
         copy_calibration()
         return
     if args.workload != "cfg1":
-        line = run_cfg2(args) if args.workload == "cfg2" else run_cfg3(args)
+        line = {"cfg2": run_cfg2, "cfg3": run_cfg3, "cfg4": run_cfg4}[args.workload](args)
         print(json.dumps(line), flush=True)
         return
     res = run_gpu(args)

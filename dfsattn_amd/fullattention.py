@@ -50,6 +50,17 @@ def dense_attention_native(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) ->
     return ops.bsa_fwd(prep, row_ptr, col_idx)
 
 
+def _sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """torch's SDPA; on the GPU restricted to its fused flash / memory-efficient
+    kernels (it raises rather than fall back to the math path)."""
+    if q.is_cuda:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v)
+    return F.scaled_dot_product_attention(q, k, v)
+
+
 def _segments(cu: Optional[torch.Tensor], total: int) -> List[Tuple[int, int]]:
     """[(start, end)] of the varlen segments of one batch row."""
     if cu is None:
@@ -79,7 +90,7 @@ def _flash(q, k, v, cu_seqlens_q, cu_seqlens_kv, batch_size):
             if (q0, q1) == (k0, k1) and q.dtype in (torch.bfloat16, torch.float16) and q.is_cuda:
                 out[bi:bi + 1, :, q0:q1] = dense_attention_native(qs, ks, vs)
             else:
-                out[bi:bi + 1, :, q0:q1] = F.scaled_dot_product_attention(qs, ks, vs)
+                out[bi:bi + 1, :, q0:q1] = _sdpa(qs, ks, vs)
     return out
 
 

@@ -8,11 +8,14 @@ diffusers ``Attention`` members the processor uses (``to_q``, ``to_k``,
 ``to_v``, ``norm_q``, ``norm_k``, ``heads``, ``add_k_proj``, ``add_v_proj``,
 ``norm_added_k``, ``to_out``); diffusers itself is not imported.
 
-The projections, QK RMSNorm and RoPE are the model's own (plain torch here,
-as in the reference's fallback path, replace_wan.py:166-218); the attention
-itself runs on this library: ``dfs_attention`` for sparse steps and
-``full_attention`` (the block-sparse kernel with every block kept) for dense
-ones, chosen as at replace_wan.py:252-308.
+The projections are the model's own. On the GPU (mode other than "flash",
+as at replace_wan.py:162, 190) the QK RMSNorm, the complex RoPE and the head
+split run in this library's fused kernel (``fused_qkv_heads``); elsewhere the
+model's norm modules and the float64 complex product of the reference's
+fallback (replace_wan.py:166-218) run in torch. The attention runs on this
+library: ``dfs_attention`` for sparse steps and ``full_attention`` (the
+block-sparse kernel with every block kept) for dense ones, chosen as at
+replace_wan.py:252-308.
 """
 from __future__ import annotations
 
@@ -31,6 +34,45 @@ def apply_rotary_emb_complex(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tens
     dtype = torch.float32 if x.device.type == "mps" else torch.float64
     xc = torch.view_as_complex(x.to(dtype).unflatten(3, (-1, 2)))
     return torch.view_as_real(xc * freqs).flatten(3, 4).type_as(x)
+
+
+def rope_tables(rotary_emb: torch.Tensor):
+    """fp32 (cos, sin) [L, D/2] of complex RoPE frequencies [.., L, D/2], the
+    conversion the reference makes for its RoPE kernel (replace_wan.py:193-198)."""
+    f = rotary_emb.reshape(-1, rotary_emb.shape[-1])
+    return f.real.to(torch.float32).contiguous(), f.imag.to(torch.float32).contiguous()
+
+
+def _norm_args(norm, channels: int, x: torch.Tensor):
+    """(weight, eps) of an RMSNorm module for the fused kernel (None: no norm)."""
+    if norm is None:
+        return None, 0.0
+    weight = getattr(norm, "weight", None)
+    if weight is None:
+        weight = torch.ones(channels, dtype=torch.float32, device=x.device)
+    eps = getattr(norm, "eps", None)
+    if eps is None:  # torch.nn.RMSNorm's default
+        eps = torch.finfo(x.dtype).eps
+    return weight.contiguous(), float(eps)
+
+
+def fused_qkv_heads(attn, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                    rotary_emb: Optional[torch.Tensor]):
+    """[B, L, H*D] projections -> [B, H, L, D] q, k, v: RMSNorm over all heads
+    (attn.norm_q / norm_k) and complex RoPE on q and k, and the head split, in
+    the library's fused kernel (one pass per tensor)."""
+    from .ops import norm_rope_heads
+
+    heads = attn.heads
+    cos = sin = None
+    if rotary_emb is not None:
+        cos, sin = rope_tables(rotary_emb)
+    wq, eq = _norm_args(attn.norm_q, query.shape[-1], query)
+    wk, ek = _norm_args(attn.norm_k, key.shape[-1], key)
+    q = norm_rope_heads(query, heads, wq, eq, cos, sin)
+    k = norm_rope_heads(key, heads, wk, ek, cos, sin)
+    v = norm_rope_heads(value, heads)
+    return q, k, v
 
 
 class Wan_DFSAttn_Processor2_0:
@@ -100,16 +142,21 @@ class Wan_DFSAttn_Processor2_0:
         query = attn.to_q(hidden_states)
         key = attn.to_k(encoder_hidden_states)
         value = attn.to_v(encoder_hidden_states)
-        if attn.norm_q is not None:
-            query = attn.norm_q(query)
-        if attn.norm_k is not None:
-            key = attn.norm_k(key)
-        query = query.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
-        key = key.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
-        value = value.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
-        if rotary_emb is not None:
-            query = apply_rotary_emb_complex(query, rotary_emb)
-            key = apply_rotary_emb_complex(key, rotary_emb)
+        if self.mode != "flash" and query.is_cuda:
+            # fused QK-RMSNorm + RoPE + head split on the GPU, where the
+            # reference runs its RMSNorm and RoPE kernels (replace_wan.py:159-205)
+            query, key, value = fused_qkv_heads(attn, query, key, value, rotary_emb)
+        else:
+            if attn.norm_q is not None:
+                query = attn.norm_q(query)
+            if attn.norm_k is not None:
+                key = attn.norm_k(key)
+            query = query.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
+            key = key.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
+            value = value.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
+            if rotary_emb is not None:
+                query = apply_rotary_emb_complex(query, rotary_emb)
+                key = apply_rotary_emb_complex(key, rotary_emb)
 
         hidden_states_img = None
         if encoder_hidden_states_img is not None:  # I2V image context (replace_wan.py:221-244)

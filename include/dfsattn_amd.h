@@ -185,6 +185,35 @@ int dfs_csr_to_mask(const int32_t* row_ptr, const int32_t* col_idx,
                     int64_t rows, int64_t k_blocks, uint8_t* mask,
                     dfs_stream_t stream);
 
+/*
+ * Fused QK RMSNorm + complex RoPE + head split of the DiT attention inputs.
+ * Element (b, l, h, d) of x is x[b*x_sb + l*x_sl + h*x_sh + d] and of out
+ * out[b*o_sb + l*o_sl + h*o_sh + d] (element strides, multiples of 8; the
+ * channel stride is 1), so x may be the projection output [B][L][H*D]
+ * (x_sh = D) and out the attention layout [B][H][L][D] (o_sh = L*D), or both
+ * the same tensor (in place). dtype (x and out): bf16 or f16.
+ *   - weight != NULL: RMSNorm over the H*D channels of each token in fp32,
+ *     y = (x * rstd) * w, rstd = 1/sqrt(sum(x^2)/(H*D) + eps), rounded to
+ *     dtype (weight_dtype bf16, f16 or f32). Replaces triton_rmsnorm_forward
+ *     (dfsattn/kernels/triton/rmsnorm.py:51) as called at
+ *     replace_wan.py:163-166.
+ *   - cos/sin != NULL: fp32 tables [L - rope_skip][D/2]; token l >= rope_skip
+ *     has each (even, odd) channel pair of every head rotated by
+ *     (cos, sin)[l - rope_skip] in float64, rounded through fp32 to dtype.
+ *     Replaces apply_qk_rope_inplace_cossin_complex
+ *     (dfsattn/kernels/csrc/ops.h:207-261, called at replace_wan.py:31-42
+ *     with len_text_prompt = rope_skip).
+ * With neither, the call is the head-split copy of replace_wan.py:181-183.
+ * heads*head_dim <= 8192, head_dim a multiple of 8.
+ */
+int dfs_norm_rope(const void* x, int64_t x_sb, int64_t x_sl, int64_t x_sh,
+                  void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh,
+                  int64_t batch, int64_t seq_len, int64_t heads,
+                  int64_t head_dim, int dtype, const void* weight,
+                  int weight_dtype, float eps, const float* cos_table,
+                  const float* sin_table, int64_t rope_skip,
+                  dfs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

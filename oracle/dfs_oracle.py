@@ -35,6 +35,14 @@ Each function restates the reference (``codesiena/DFSattn``) at the cited
   attention_hyvideo.py:1054-1082): pinned against dense attention under an
   explicit block-diagonal token mask whose blocks are counted from each
   segment's start.
+* ``rmsnorm_rows`` (kernels/triton/rmsnorm.py:9-48): pinned against
+  ``torch.nn.functional.rms_norm`` (the library routine) in fp32 and within
+  one bf16 unit in the last place after rounding.
+* ``rope_complex_pairs`` (rope_enc_complex.cuh, ops.h:207-261): pinned
+  bit-exactly against the reference's own torch fallback, a complex128
+  product through ``torch.view_as_complex`` (replace_wan.py:209-213), and by
+  the rotation invariants (angle 0 is the identity, pair norms are kept,
+  rotating by -angle undoes +angle).
 """
 from __future__ import annotations
 
@@ -467,3 +475,45 @@ def dfs_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, v
     else:
         out = segment_attention(qp, kp, vp, mask, [0, valid, seq_len], block)
     return out[:, :, inv, :], mask, scores
+
+
+# --------------------------------------------------------------------------
+# DiT attention inputs: QK RMSNorm, complex RoPE, head split
+# (kernels/triton/rmsnorm.py:9-48; kernels/include/rope/rope_enc_complex.cuh;
+# replace_wan.py:159-218)
+# --------------------------------------------------------------------------
+
+def rmsnorm_rows(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm over the last axis as the reference's fused kernel computes it
+    (rmsnorm.py:28-44): x in fp32, var = sum(x*x)/N, rstd = 1/sqrt(var+eps),
+    y = (x*rstd)*w in fp32, stored in x's dtype."""
+    xf = x.float()
+    var = (xf * xf).sum(-1, keepdim=True) / xf.shape[-1]
+    rstd = 1.0 / torch.sqrt(var + eps)
+    return ((xf * rstd) * weight.float()).to(x.dtype)
+
+
+def rope_complex_pairs(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotation of the (even, odd) channel pairs of x [..., L, D] by fp32
+    (cos, sin) [L, D/2] (rope_enc_complex.cuh: out[2i] = x[2i] c - x[2i+1] s,
+    out[2i+1] = x[2i+1] c + x[2i] s in float64), rounded float64 -> float32 ->
+    x's dtype."""
+    xd = x.double()
+    c, s = cos.double(), sin.double()
+    xe, xo = xd[..., 0::2], xd[..., 1::2]
+    out = torch.stack([xe * c - xo * s, xo * c + xe * s], dim=-1).flatten(-2)
+    return out.float().to(x.dtype)
+
+
+def norm_rope_heads(x: torch.Tensor, heads: int, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                    cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                    rope_skip: int = 0) -> torch.Tensor:
+    """[B, L, H*D] -> [B, H, L, D]: RMSNorm over all channels (if weight),
+    head split (replace_wan.py:181-183), RoPE of tokens l >= rope_skip by
+    row l - rope_skip of the tables (if cos)."""
+    y = rmsnorm_rows(x, weight, eps) if weight is not None else x
+    y = y.unflatten(-1, (heads, -1)).transpose(1, 2).contiguous()
+    if cos is not None:
+        y = y.clone()
+        y[:, :, rope_skip:] = rope_complex_pairs(y[:, :, rope_skip:], cos, sin)
+    return y

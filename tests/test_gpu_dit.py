@@ -1,0 +1,188 @@
+"""GPU parity of the fused QK-RMSNorm + RoPE + head-split kernel against the
+oracle, and of whole DiT forwards (the small model of the cfg4 structure)
+against fp32 references on the host."""
+import pytest
+import torch
+
+from oracle import dfs_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(out, ref):
+    return float((out.double() - ref.double()).abs().mean() / ref.double().abs().mean())
+
+
+def _ulps(a, b):
+    ai = a.contiguous().view(torch.int16).to(torch.int32)
+    bi = b.contiguous().view(torch.int16).to(torch.int32)
+    return (ai - bi).abs()
+
+
+@pytest.fixture(autouse=True)
+def _clean():
+    from dfsattn_amd import attention_wan as wat
+    wat.DFS_Attention.clear_cache()
+    wat._dfs_attention_instances.clear()
+    yield
+    wat.DFS_Attention.clear_cache()
+    wat._dfs_attention_instances.clear()
+
+
+CASES = [
+    # B, L, H, D, dtype, weight dtype (None: no norm), rope, rope_skip
+    (1, 300, 4, 128, torch.bfloat16, torch.bfloat16, True, 0),
+    (2, 77, 3, 64, torch.float16, torch.float32, True, 5),
+    (1, 64, 40, 128, torch.bfloat16, torch.bfloat16, True, 0),  # C = 5120 (Wan 14B)
+    (1, 50, 24, 128, torch.bfloat16, torch.float16, False, 0),  # norm only, C = 3072
+    (1, 129, 2, 128, torch.bfloat16, None, True, 0),  # rope only
+    (3, 33, 5, 64, torch.float16, None, False, 0),  # head split only
+]
+
+
+@pytest.mark.parametrize("B,L,H,D,dtype,wdt,rope,skip", CASES)
+def test_norm_rope_heads_matches_oracle(dev, B, L, H, D, dtype, wdt, rope, skip):
+    from dfsattn_amd import ops
+    print(f"norm_rope B={B} L={L} H={H} D={D} {dtype} w={wdt} rope={rope} skip={skip}", flush=True)
+    g = torch.Generator().manual_seed(L * H + D)
+    x = (torch.randn(B, L, H * D, generator=g) * 3).to(dtype)
+    w = None if wdt is None else (torch.rand(H * D, generator=g) + 0.5).to(wdt)
+    cos = sin = None
+    if rope:
+        ang = torch.rand(L - skip, D // 2, generator=g, dtype=torch.float64) * 50
+        cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    ref = orc.norm_rope_heads(x, H, w, 1e-6, cos, sin, skip)
+    got = ops.norm_rope_heads(x.to(dev), H, None if w is None else w.to(dev), 1e-6,
+                              None if cos is None else cos.to(dev), None if sin is None else sin.to(dev), skip)
+    got = got.cpu()
+    assert got.shape == (B, H, L, D) and got.dtype == dtype
+    if w is None:
+        assert torch.equal(got, ref)  # no reduction: bit-exact
+        return
+    # the sum of squares is reduced in another order than the oracle's, so a
+    # normalised value can differ by one unit in the last place (ulp); almost
+    # every element is identical
+    assert float((got == ref).float().mean()) > 0.99
+    if not rope:
+        assert int(_ulps(got, ref).max()) <= 1
+        return
+    # the rotation moves a one-ulp input difference into the output without
+    # growing it: |diff| <= ulp of the pair's magnitude + one output ulp
+    mant = 7 if dtype == torch.bfloat16 else 10
+    r = ref.float()
+    pair = torch.sqrt(r[..., 0::2] ** 2 + r[..., 1::2] ** 2).repeat_interleave(2, dim=-1)
+    tol = 2.0 ** -mant * (pair + r.abs()) + 1e-6
+    assert bool(((got.float() - r).abs() <= tol).all())
+
+
+def test_norm_rope_in_place_on_attention_layout(dev):
+    """RoPE in place on a [B, H, S, D] tensor (the layout of the reference's
+    apply_qk_rope_inplace_cossin_complex) with a skipped prefix."""
+    from dfsattn_amd import ops
+    g = torch.Generator().manual_seed(21)
+    B, H, S, D, skip = 2, 3, 90, 128, 10
+    q = torch.randn(B, H, S, D, generator=g).bfloat16()
+    ang = torch.rand(S - skip, D // 2, generator=g, dtype=torch.float64) * 10
+    cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    qd = q.to(dev)
+    view = qd.permute(0, 2, 1, 3)  # [B, S, H, D] view of the same memory
+    ops.norm_rope(view, view, cos=cos.to(dev), sin=sin.to(dev), rope_skip=skip)
+    ref = q.clone()
+    ref[:, :, skip:] = orc.rope_complex_pairs(q[:, :, skip:], cos, sin)
+    assert torch.equal(qd.cpu(), ref)
+
+
+def test_norm_rope_rejects_bad_arguments(dev):
+    from dfsattn_amd import ops
+    from dfsattn_amd._lib import DfsKernelError
+    x = torch.zeros(1, 8, 2 * 128, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        ops.norm_rope_heads(x, 2, torch.ones(100, device=dev))
+    with pytest.raises(ValueError):
+        ops.norm_rope_heads(x, 2, cos=torch.ones(8, 64, device=dev))
+    big = torch.zeros(1, 2, 72 * 128, dtype=torch.bfloat16, device=dev)  # 9216 channels > 8192
+    with pytest.raises(DfsKernelError):
+        ops.norm_rope_heads(big, 72)
+
+
+def _tiny(dev):
+    from dfsattn_amd import dit
+    cfg = dit.DIT_CONFIGS["tiny"]
+    model = dit.build_model(cfg, dev)
+    latent, ctx, _ = dit.synth_inputs(cfg, dev)
+    return cfg, model, latent, ctx
+
+
+@torch.no_grad()
+def test_fused_processor_path_matches_torch_path(dev):
+    """A dense step of the small DiT with the fused QK-norm/RoPE kernel
+    (mode "dfs") against the same step through the model's torch norm
+    modules and the float64 complex RoPE (mode "flash")."""
+    from dfsattn_amd import dit
+    cfg, model, latent, ctx = _tiny(dev)
+    t = torch.tensor([300.0], device=dev)
+    procs = dit.install_dfs_processors(model, "dfs")
+    dit.set_step(procs, 0)  # real step 0 < skip_steps: dense
+    fused = model(latent, t, ctx)
+    dit.install_dfs_processors(model, "flash")
+    plain = model(latent, t, ctx)
+    assert bool(torch.isfinite(fused).all())
+    assert _rel(fused.cpu(), plain.cpu()) < 1e-2
+
+
+class _RefProcessor:
+    """fp32 host attention for the reference model: the torch QK norm and
+    complex RoPE, then masked attention over a given block mask in the
+    given token order (self-attention) or dense attention (cross)."""
+
+    def __init__(self, mask=None, perm=None, inv=None):
+        self.mask, self.perm, self.inv = mask, perm, inv
+
+    def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, rotary_emb=None):
+        from dfsattn_amd.replace_wan import apply_rotary_emb_complex
+        enc = hidden_states if encoder_hidden_states is None else encoder_hidden_states
+        q = attn.norm_q(attn.to_q(hidden_states)).unflatten(2, (attn.heads, -1)).transpose(1, 2)
+        k = attn.norm_k(attn.to_k(enc)).unflatten(2, (attn.heads, -1)).transpose(1, 2)
+        v = attn.to_v(enc).unflatten(2, (attn.heads, -1)).transpose(1, 2)
+        if rotary_emb is not None:
+            q = apply_rotary_emb_complex(q, rotary_emb)
+            k = apply_rotary_emb_complex(k, rotary_emb)
+        if self.mask is None:
+            o = orc.dense_attention(q, k, v)
+        else:
+            p = self.perm
+            o = orc.masked_attention(orc.apply_permutation(q, p), orc.apply_permutation(k, p),
+                                     orc.apply_permutation(v, p), self.mask)[:, :, self.inv]
+        return attn.to_out[0](o.transpose(1, 2).flatten(2, 3))
+
+
+@torch.no_grad()
+def test_dit_sparse_step_matches_fp32_reference(dev):
+    """A DFS refresh step of the small DiT on the GPU (bf16, fused kernels,
+    fresh masks) against the same weights in fp32 on the host with the
+    attention recomputed over the masks the GPU selected."""
+    from dfsattn_amd import dit
+    from dfsattn_amd.attention_wan import DFS_Attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    cfg, model, latent, ctx = _tiny(dev)
+    t = torch.tensor([700.0], device=dev)
+    perm = hilbert3d_perm(*cfg.grid)
+    procs = dit.install_dfs_processors(model, "dfs", 0.3, 16, 128, perm, skip_steps=12, cache_interval=12)
+    dit.set_step(procs, 24)  # real step 12: mask refresh
+    out = model(latent, t, ctx).cpu()
+    masks = {key[0]: e["block_mask"].cpu() for key, e in DFS_Attention._cached_metadata.items()}
+    assert sorted(masks) == [2 * i for i in range(cfg.layers)]
+    kb = (cfg.seq_len + 127) // 128
+    for m in masks.values():
+        assert bool((m.sum(-1) == max(1, int(0.3 * kb))).all())  # sparse rows of the Wan policy
+
+    ref_model = dit.WanLikeDiT(cfg, device="cpu", dtype=torch.float32).eval()
+    ref_model.load_state_dict({k: v.float().cpu() for k, v in model.state_dict().items()})
+    full, inv = orc.full_permutation(perm, cfg.seq_len)
+    for i, (name, module) in enumerate(ref_model.attention_modules()):
+        module.set_processor(_RefProcessor() if "attn2" in name else _RefProcessor(masks[i], full, inv))
+    ref = ref_model(latent.cpu(), t.cpu(), ctx.cpu())
+    assert bool(torch.isfinite(out).all())
+    rel = _rel(out, ref)
+    print(f"tiny DiT sparse step vs fp32 host reference: mean-rel {rel:.2e}", flush=True)
+    assert rel < 3e-2

@@ -210,3 +210,66 @@ def test_axis_and_block_oracles_closed_forms():
     blk = orc.block3d_perm(2, 2, 4, 1, 2, 2)  # bricks of 1x2x2 over a 2x2x4 grid
     assert blk.tolist() == [0, 1, 4, 5, 2, 3, 6, 7, 8, 9, 12, 13, 10, 11, 14, 15]
     assert sorted(orc.block3d_perm(5, 3, 9, 4, 4, 4).tolist()) == list(range(135))
+
+
+# ---- DiT attention inputs: RMSNorm and complex RoPE
+def _bf16_ulps(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """Distance in bf16 units in the last place (same-sign finite values)."""
+    ai = a.view(torch.int16).to(torch.int32)
+    bi = b.view(torch.int16).to(torch.int32)
+    return (ai - bi).abs()
+
+
+def test_rmsnorm_oracle_matches_library():
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(37, 640, generator=g) * 3
+    w = torch.randn(640, generator=g)
+    torch.testing.assert_close(orc.rmsnorm_rows(x, w, 1e-6), F.rms_norm(x, (640,), w, 1e-6), rtol=3e-6, atol=3e-6)
+    # eps matters on small rows, as in the library
+    tiny = x[:2] * 1e-4
+    torch.testing.assert_close(orc.rmsnorm_rows(tiny, w, 1e-6), F.rms_norm(tiny, (640,), w, 1e-6),
+                               rtol=3e-6, atol=1e-9)
+    xb, wb = x.bfloat16(), w.bfloat16()
+    got = orc.rmsnorm_rows(xb, wb, 1e-6)
+    ref = F.rms_norm(xb.float(), (640,), wb.float(), 1e-6).bfloat16()
+    same_sign = torch.sign(got.float()) == torch.sign(ref.float())
+    assert bool(same_sign.all()) and int(_bf16_ulps(got, ref).max()) <= 1
+    assert float((got == ref).float().mean()) > 0.99
+
+
+def test_rope_oracle_matches_complex_product():
+    g = torch.Generator().manual_seed(12)
+    x = (torch.randn(2, 3, 50, 128, generator=g) * 2).bfloat16()
+    ang = torch.rand(50, 64, generator=g, dtype=torch.float64) * 40
+    cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    # the reference's fallback: complex128 product of view_as_complex pairs (replace_wan.py:209-213)
+    freqs = torch.complex(cos.double(), sin.double())
+    ref = torch.view_as_real(torch.view_as_complex(x.double().unflatten(-1, (-1, 2))) * freqs).flatten(-2)
+    assert torch.equal(orc.rope_complex_pairs(x, cos, sin), ref.float().bfloat16())
+    assert torch.equal(orc.rope_complex_pairs(x, torch.ones_like(cos), torch.zeros_like(sin)), x)
+    # rotation keeps pair norms and -angle undoes +angle
+    xf = x.float()
+    r = orc.rope_complex_pairs(xf, cos, sin)
+    n0 = xf[..., 0::2] ** 2 + xf[..., 1::2] ** 2
+    n1 = r[..., 0::2] ** 2 + r[..., 1::2] ** 2
+    torch.testing.assert_close(n1, n0, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(orc.rope_complex_pairs(r, cos, -sin), xf, rtol=1e-5, atol=1e-5)
+    # a known rotation: angle pi/2 maps (a, b) to (-b, a)
+    quarter = orc.rope_complex_pairs(xf[..., :1, :], torch.zeros(1, 64), torch.ones(1, 64))
+    assert torch.equal(quarter[..., 0::2], -xf[..., :1, 1::2]) and torch.equal(quarter[..., 1::2], xf[..., :1, 0::2])
+
+
+def test_norm_rope_heads_oracle_layout():
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(2, 9, 3 * 16, generator=g).bfloat16()
+    w = torch.rand(48, generator=g) + 0.5
+    cos, sin = torch.rand(6, 8, generator=g), torch.rand(6, 8, generator=g)
+    out = orc.norm_rope_heads(x, 3, w, 1e-6, cos, sin, rope_skip=3)
+    assert out.shape == (2, 3, 9, 16)
+    normed = orc.rmsnorm_rows(x, w, 1e-6)
+    for b in range(2):
+        for h in range(3):
+            head = normed[b, :, h * 16:(h + 1) * 16]
+            assert torch.equal(out[b, h, :3], head[:3])  # rows before rope_skip are not rotated
+            assert torch.equal(out[b, h, 3:], orc.rope_complex_pairs(head[3:], cos, sin))
