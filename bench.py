@@ -301,10 +301,12 @@ def run_cfg4(args):
         log(f"{label} step: {ms:.1f} ms")
         return ms
 
-    sparse_ms = timed(24, "DFS (s=0.3, refresh)")
-    dense_ms = timed(0, "dense")
+    sparse_ms = timed(24, "DFS (s=0.3, refresh)") if args.dit_phase in ("both", "dfs") else None
+    dense_ms = timed(0, "dense") if args.dit_phase in ("both", "dense") else None
     DFS_Attention.clear_cache()
     _dfs_attention_instances.clear()
+    if sparse_ms is None:
+        sparse_ms = float("nan")
     return {"metric": "DiT denoising step ms (40 blocks, 75.6k tok, d5120, CFG) with DFS self-attention s=0.3",
             "value": round(sparse_ms, 1), "unit": "ms/step", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(sparse_ms, 1), "higher_is_better": False,
@@ -314,7 +316,8 @@ def run_cfg4(args):
                                    "QK-RMSNorm + 3D RoPE, 512x4096 text context, latent 21x45x80 tokens, "
                                    "conditional + unconditional pass, DFS refresh step (fresh masks)",
                        "global_batch": 1, "seq_len": cfg.seq_len, "parallelism": "none (1 GPU)"},
-            "dense_step_ms": round(dense_ms, 1), "speedup_vs_dense": round(dense_ms / sparse_ms, 3),
+            "dense_step_ms": None if dense_ms is None else round(dense_ms, 1),
+            "speedup_vs_dense": round(dense_ms / sparse_ms, 3) if sparse_ms and dense_ms else None,
             "params": cfg.params()}
 
 
@@ -401,6 +404,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", choices=("cfg1", "cfg2", "cfg3", "cfg4"), default="cfg1")
+    ap.add_argument("--dit-phase", choices=("both", "dfs", "dense"), default="both",
+                    help="cfg4: time the DFS step, the dense step or both")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = 2 if args.workload == "cfg4" else 20

@@ -24,7 +24,7 @@
 namespace dfs {
 namespace {
 
-constexpr int kMaxChunks = 16;  // 16 x 512 channels per row
+constexpr int kMaxChunks = 16;  // at most 16 x 512 channels per row
 
 struct NormRopeParams {
   int64_t x_sb, x_sl, x_sh;  // element strides of x (channel stride 1)
@@ -53,6 +53,11 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// NCH: 512-channel chunks held per lane (the smallest even count that covers
+// the row: 10 for 5,120 channels). The weights and the RoPE table row are fetched together
+// with x, before the reduction, so no second memory round trip sits
+// between the reduction and the stores.
+template <int NCH>
 __global__ void __launch_bounds__(256) norm_rope_kernel(const uint16_t* x, uint16_t* out,  // may alias (in place)
                                                         const void* __restrict__ weight,
                                                         const float* __restrict__ cos_t,
@@ -64,16 +69,37 @@ __global__ void __launch_bounds__(256) norm_rope_kernel(const uint16_t* x, uint1
   const int l = static_cast<int>(row - b * p.L);
   const uint16_t* xr = x + b * p.x_sb + static_cast<int64_t>(l) * p.x_sl;
   uint16_t* orow = out + b * p.o_sb + static_cast<int64_t>(l) * p.o_sl;
+  const bool norm = p.w_dtype >= 0;
+  const int lr = l - p.rope_skip;
+  const bool rope = cos_t != nullptr && lr >= 0;
+  const int half = p.D >> 1;
+  // 512 % D == 0 (D = 64, 128, ...): every chunk of a lane has the same
+  // channel d, so one (cos, sin) row slice serves all of them
+  const bool same_d = (512 % p.D) == 0;
 
-  uint4 v[kMaxChunks];
-  float ss = 0.f;
+  uint4 v[NCH];
+  uint4 wv[NCH];  // bf16/f16 weights
+  float4 cs_same = make_float4(0.f, 0.f, 0.f, 0.f), sn_same = cs_same;
+  if (rope && same_d) {
+    const int d0 = (lane * 8) % p.D;
+    cs_same = *reinterpret_cast<const float4*>(cos_t + static_cast<int64_t>(lr) * half + (d0 >> 1));
+    sn_same = *reinterpret_cast<const float4*>(sin_t + static_cast<int64_t>(lr) * half + (d0 >> 1));
+  }
 #pragma unroll
-  for (int j = 0; j < kMaxChunks; ++j) {
+  for (int j = 0; j < NCH; ++j) {
     const int e = j * 512 + lane * 8;
-    if (j < p.nch && e < p.C) {
+    if (e < p.C) {
       const int h = e / p.D, d = e - h * p.D;
       v[j] = *reinterpret_cast<const uint4*>(xr + h * p.x_sh + d);
-      if (p.w_dtype >= 0) {
+      if (norm && p.w_dtype != DFS_DTYPE_F32) wv[j] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(weight) + e);
+    }
+  }
+  float rstd = 1.f;
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      if (j * 512 + lane * 8 < p.C) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float f = to_f32(u16_at(v[j], i), p.dtype);
@@ -81,25 +107,19 @@ __global__ void __launch_bounds__(256) norm_rope_kernel(const uint16_t* x, uint1
         }
       }
     }
-  }
-  float rstd = 1.f;
-  if (p.w_dtype >= 0) {
     const float var = wave_sum(ss) / static_cast<float>(p.C);
     rstd = 1.0f / sqrtf(var + p.eps);
   }
-  const int lr = l - p.rope_skip;
-  const bool rope = cos_t != nullptr && lr >= 0;
-  const int half = p.D >> 1;
 
 #pragma unroll
-  for (int j = 0; j < kMaxChunks; ++j) {
+  for (int j = 0; j < NCH; ++j) {
     const int e = j * 512 + lane * 8;
-    if (!(j < p.nch && e < p.C)) continue;
+    if (e >= p.C) continue;
     const int h = e / p.D, d = e - h * p.D;
     float y[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = to_f32(u16_at(v[j], i), p.dtype);
-    if (p.w_dtype >= 0) {
+    if (norm) {
       float w[8];
       if (p.w_dtype == DFS_DTYPE_F32) {
         const float4 w0 = *reinterpret_cast<const float4*>(static_cast<const float*>(weight) + e);
@@ -107,9 +127,8 @@ __global__ void __launch_bounds__(256) norm_rope_kernel(const uint16_t* x, uint1
         w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
         w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
       } else {
-        const uint4 wb = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(weight) + e);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = to_f32(u16_at(wb, i), p.w_dtype);
+        for (int i = 0; i < 8; ++i) w[i] = to_f32(u16_at(wv[j], i), p.w_dtype);
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -118,8 +137,11 @@ __global__ void __launch_bounds__(256) norm_rope_kernel(const uint16_t* x, uint1
       }
     }
     if (rope) {
-      const float4 c4 = *reinterpret_cast<const float4*>(cos_t + static_cast<int64_t>(lr) * half + (d >> 1));
-      const float4 s4 = *reinterpret_cast<const float4*>(sin_t + static_cast<int64_t>(lr) * half + (d >> 1));
+      float4 c4 = cs_same, s4 = sn_same;
+      if (!same_d) {
+        c4 = *reinterpret_cast<const float4*>(cos_t + static_cast<int64_t>(lr) * half + (d >> 1));
+        s4 = *reinterpret_cast<const float4*>(sin_t + static_cast<int64_t>(lr) * half + (d >> 1));
+      }
       const float cs[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -190,8 +212,28 @@ extern "C" int dfs_norm_rope(const void* x, int64_t x_sb, int64_t x_sl, int64_t 
   DFS_REQUIRE(seq_len < (int64_t(1) << 31), "norm_rope: seq_len too large");
   const int64_t blocks = (p.rows + 3) / 4;
   DFS_REQUIRE(blocks < (int64_t(1) << 31), "norm_rope: too many rows");
-  hipLaunchKernelGGL(norm_rope_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
-                     static_cast<uint16_t*>(out), weight, cos_table, sin_table, p);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const uint16_t* xs = static_cast<const uint16_t*>(x);
+  uint16_t* os = static_cast<uint16_t*>(out);
+  switch ((p.nch + 1) / 2) {  // smallest even chunk count that covers the row
+#define DFS_NORM_ROPE_CASE(HALF)                                                                        \
+  case HALF:                                                                                           \
+    hipLaunchKernelGGL(norm_rope_kernel<2 * HALF>, grid, block, 0, st, xs, os, weight, cos_table, sin_table, \
+                       p);                                                                             \
+    break;
+    DFS_NORM_ROPE_CASE(1)
+    DFS_NORM_ROPE_CASE(2)
+    DFS_NORM_ROPE_CASE(3)
+    DFS_NORM_ROPE_CASE(4)
+    DFS_NORM_ROPE_CASE(5)
+    DFS_NORM_ROPE_CASE(6)
+    DFS_NORM_ROPE_CASE(7)
+    DFS_NORM_ROPE_CASE(8)
+#undef DFS_NORM_ROPE_CASE
+    default:
+      set_error("norm_rope: internal chunk count %d", p.nch);
+      return 1;
+  }
   return check_launch("norm_rope");
 }
