@@ -37,6 +37,8 @@ CASES = [
     (1, 50, 24, 128, torch.bfloat16, torch.float16, False, 0),  # norm only, C = 3072
     (1, 129, 2, 128, torch.bfloat16, None, True, 0),  # rope only
     (3, 33, 5, 64, torch.float16, None, False, 0),  # head split only
+    (1, 40, 1, 5120, torch.bfloat16, torch.bfloat16, False, 0),  # one 5,120-wide "head": a plain row norm
+    (1, 20, 3, 96, torch.bfloat16, None, True, 0),  # 512 % D != 0: the table slice moves per chunk
 ]
 
 
