@@ -281,6 +281,73 @@ __device__ __forceinline__ void pv_tile_log2(const uint16_t* v_tile, const f32x1
   }
 }
 
+// Scheduling of an MFMA phase: the LDS operand reads run kAhead MFMAs ahead
+// of their MFMAs, so each read's latency is covered by the MFMAs before its
+// use (in the ping-pong schedule the other wave on the SIMD is doing VALU
+// work and cannot fill MFMA gaps; in the split schedule the two waves of a
+// SIMD come from independent workgroups and often read at the same time).
+// Pinned with scheduling-group barriers:
+// kAhead reads, then alternately one MFMA and one read, then the last MFMAs.
+constexpr int kAhead = 4;
+template <int N>
+__device__ __forceinline__ void pin_read_ahead_schedule() {
+  constexpr int kMfma = 0x008, kDsRead = 0x100;
+  __builtin_amdgcn_sched_group_barrier(kDsRead, kAhead, 0);
+#pragma unroll
+  for (int i = 0; i < N - kAhead; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(kMfma, kAhead, 0);
+}
+
+// O^T += V^T P^T from an LDS V^T tile and P held in registers.
+template <int D>
+__device__ __forceinline__ void pv_tile_regs(const uint16_t* v_tile, const f16x8* pf, f32x16* o, int l32, int hl) {
+  constexpr int DCH = D / 32, N = 8 * DCH;
+  uint4 a[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) a[i] = lds_chunk<16>(v_tile, (i % DCH) * 32 + l32, (i / DCH) * 2 + hl);
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    o[i % DCH] = MfmaOp<true>::run(__builtin_bit_cast(f16x8, a[i]), pf[i / DCH], o[i % DCH]);
+  pin_read_ahead_schedule<N>();
+}
+
+// S^T = init + K Q^T from an LDS K tile, with the read-ahead schedule above.
+template <int D>
+__device__ __forceinline__ void qk_tile_ahead(const uint16_t* k_tile, const f16x8* qf, int l32, int hl, f32x16* s,
+                                              const f32x16& init = f32x16{}) {
+  constexpr int CPR = D / 8, DS = D / 16, N = 4 * DS;
+  uint4 a[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) a[i] = lds_chunk<CPR>(k_tile, (i / DS) * 32 + l32, (i % DS) * 2 + hl);
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc) s[kc] = init;
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    s[i / DS] = MfmaOp<true>::run(__builtin_bit_cast(f16x8, a[i]), qf[i % DS], s[i / DS]);
+  pin_read_ahead_schedule<N>();
+}
+
+// P = exp2(S') of a whole block as f16 PV operands; lblk receives this lane's
+// share of the block's row sum (of the rounded values).
+__device__ __forceinline__ void make_p(const f32x16* s, f16x8* pf, float& lblk) {
+  lblk = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    const f32x16& src = s[ks >> 1];
+    const int r0 = (ks & 1) * 8;
+    f16x2 pr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pr[j] = MfmaOp<true>::pack(exp2_fast(src[r0 + 2 * j]), exp2_fast(src[r0 + 2 * j + 1]));
+      lblk = MfmaOp<true>::sum2(pr[j], lblk);
+    }
+    pf[ks] = __builtin_bit_cast(f16x8, pr);
+  }
+}
+
 // O = O^T / l for row qrow, columns d = dc*32 + g*8 + hl*4 + (0..3); rows past
 // L are dropped, rows with no kept block give 0.
 template <int D>
@@ -471,7 +538,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
       block_barrier();        // ... and everybody else's
       f32x16 s[4];
       if constexpr (QK_F16)
-        qk_tile<D, QkOp>(k_lds, qf, l32, hl, s, negm);
+        qk_tile_ahead<D>(k_lds, qf, l32, hl, s, negm);
       else
         qk_tile<D, QkOp>(k_lds, qf, l32, hl, s);
       block_barrier();  // K tile fully consumed
@@ -481,9 +548,27 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
         asm volatile("" : "+s"(valid));  // compares stay in this (rare) branch
         mask_tail(s, valid, hl);
       }
-      if constexpr (QK_F16) {
-        softmax_lazy<DCH>(s, t == 0, m, lsum, o, negm);
+      if constexpr (QK_F16 && PV_F16) {
+        // The row reference m is set from the first block's maximum. Later
+        // blocks skip the maximum: P = exp2(S - m) is formed directly and
+        // accepted unless it overflows f16 (some S - m >= 16, which turns
+        // the block's row sum inf); only then is the block redone with a
+        // moved reference. P <= 2^16 keeps f16's 11-bit precision.
+        if (t == 0) softmax_lazy<DCH>(s, true, m, lsum, o, negm);
+        f16x8 pf[8];
+        float lblk;
+        make_p(s, pf, lblk);
+        if (t > 0 && __any(!(lblk < INFINITY))) {
+          softmax_lazy<DCH>(s, false, m, lsum, o, negm);
+          make_p(s, pf, lblk);
+        }
+        lsum += lblk;
         wait_vmcnt<K_LOADS>();  // V copies landed (the next K may be in flight)
+        block_barrier();
+        pv_tile_regs<D>(v_lds, pf, o, l32, hl);
+      } else if constexpr (QK_F16) {
+        softmax_lazy<DCH>(s, t == 0, m, lsum, o, negm);
+        wait_vmcnt<K_LOADS>();
         block_barrier();
         pv_tile_log2<D, PvOp>(v_lds, s, lsum, o, l32, hl);
       } else {
@@ -582,51 +667,6 @@ __device__ __forceinline__ void pp_softmax_second(const f32x16* s, float m, floa
   }
 }
 
-// Scheduling of an MFMA phase: the LDS operand reads run kAhead MFMAs ahead
-// of their MFMAs, so each read's latency is covered by the MFMAs before its
-// use (in the ping-pong schedule the other wave on the SIMD is doing VALU
-// work and cannot fill MFMA gaps). Pinned with scheduling-group barriers:
-// kAhead reads, then alternately one MFMA and one read, then the last MFMAs.
-constexpr int kAhead = 4;
-template <int N>
-__device__ __forceinline__ void pin_read_ahead_schedule() {
-  constexpr int kMfma = 0x008, kDsRead = 0x100;
-  __builtin_amdgcn_sched_group_barrier(kDsRead, kAhead, 0);
-#pragma unroll
-  for (int i = 0; i < N - kAhead; ++i) {
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(kMfma, kAhead, 0);
-}
-
-// O^T += V^T P^T from an LDS V^T tile and P held in registers.
-template <int D>
-__device__ __forceinline__ void pv_tile_regs(const uint16_t* v_tile, const f16x8* pf, f32x16* o, int l32, int hl) {
-  constexpr int DCH = D / 32, N = 8 * DCH;
-  uint4 a[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) a[i] = lds_chunk<16>(v_tile, (i % DCH) * 32 + l32, (i / DCH) * 2 + hl);
-#pragma unroll
-  for (int i = 0; i < N; ++i)
-    o[i % DCH] = MfmaOp<true>::run(__builtin_bit_cast(f16x8, a[i]), pf[i / DCH], o[i % DCH]);
-  pin_read_ahead_schedule<N>();
-}
-
-// S^T = K Q^T from an LDS K tile, with the read-ahead schedule above.
-template <int D>
-__device__ __forceinline__ void qk_tile_ahead(const uint16_t* k_tile, const f16x8* qf, int l32, int hl, f32x16* s) {
-  constexpr int CPR = D / 8, DS = D / 16, N = 4 * DS;
-  uint4 a[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) a[i] = lds_chunk<CPR>(k_tile, (i / DS) * 32 + l32, (i % DS) * 2 + hl);
-#pragma unroll
-  for (int kc = 0; kc < 4; ++kc) s[kc] = f32x16{};
-#pragma unroll
-  for (int i = 0; i < N; ++i)
-    s[i / DS] = MfmaOp<true>::run(__builtin_bit_cast(f16x8, a[i]), qf[i % DS], s[i / DS]);
-  pin_read_ahead_schedule<N>();
-}
 
 // Ping-pong schedule (f16 operands). One workgroup of eight
 // waves per CU serves two adjacent query blocks of a head: waves 0-3 (group
