@@ -96,6 +96,18 @@ def run_gpu(args):
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ms_per_step = e0.elapsed_time(e1) / args.steps
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/call")
+    # Median of per-call event pairs over at least 50 further calls.
+    per_call = []
+    for _ in range(max(50, args.steps)):
+        a, b = _events()
+        a.record()
+        step()
+        b.record()
+        per_call.append((a, b))
+    torch.cuda.synchronize()
+    per_call = sorted(a.elapsed_time(b) for a, b in per_call)
+    median_ms = per_call[len(per_call) // 2]
+    log(f"median of {len(per_call)} calls: {median_ms:.3f} ms")
 
     # Per-kernel times of the same call, each bracketed by events on the
     # stream the kernels run on (the current stream), averaged over steps.
@@ -130,6 +142,8 @@ def run_gpu(args):
     _dfs_attention_instances.clear()
     return {
         "ms_per_step": ms_per_step,
+        "median_ms": median_ms,
+        "median_calls": len(per_call),
         "wall_ms_per_step": wall_ms,
         "phase_ms": phase_ms,
         "attention_flop": flops,
@@ -451,6 +465,8 @@ def main():
                      "frac": round(res["attention_tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic(),
                      "kernel": "bsa_fwd_split_kernel", "kernel_ms": round(att_ms, 3),
                      "algorithmic_flop": res["attention_flop"]},
+        "median_ms_per_call": round(res["median_ms"], 3),
+        "median_of_calls": res["median_calls"],
         "phases_ms": {k_: round(v_, 3) for k_, v_ in res["phase_ms"].items()},
         "prepare_gbs": round(res["prepare_gbs"], 1),
         "kept_density": round(res["density"], 4),
