@@ -221,11 +221,12 @@ __device__ __forceinline__ void load_q_scaled(const uint16_t* __restrict__ q, co
 }
 
 // Lazy online softmax on S' = S c - m, where the running reference m enters
-// through the QK MFMA's C input (negm holds -m in every element). m moves
-// only when some row of the wave sees a block maximum above m + kLazyTau, or
-// on the row's first block, so P = exp2(S') stays <= 2^kLazyTau (f16 holds
-// it exactly to 11 bits) and O and l are rarely rescaled. The result is the
-// same softmax: numerator and denominator share the reference.
+// through the QK MFMA's C input (negm holds -m in every element). On a row's
+// first block m becomes the block maximum; later, m moves only when some row
+// of the wave sees a block maximum above m + kLazyTau, and O and l are
+// rescaled then. The result is the same softmax: numerator and denominator
+// share the reference. (With f16 P the split kernel calls this only for a
+// row's first block and for a block whose P overflowed f16.)
 constexpr float kLazyTau = 8.0f;
 template <int DCH>
 __device__ __forceinline__ void softmax_lazy(f32x16* s, bool first, float& m, float& lsum, f32x16* o,

@@ -353,8 +353,13 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     };
 
     issue(0);
-    // Pass 1: running max and normaliser (log2 domain) of every query tile,
-    // one per lane half.
+    // Pass 1: normaliser z of every query tile (one per lane half) against a
+    // reference m in the log2 domain: m is the maximum of the tile's first
+    // chunk; later chunks add exp2(s - m) without a maximum, and only a
+    // chunk whose sum exceeds 2^64 (some s - m > 64) moves m. Any reference
+    // gives the same softmax; with terms at most 2^64 and fp32's range down
+    // to 2^-126 nothing of weight is lost and no block sum can overflow.
+    // Only the last chunk can hold key tiles past the end.
     float m = -INFINITY, z = 0.f;
     for (int c = 0; c < nchunks; ++c) {
       wait_vmcnt_0();
@@ -362,21 +367,36 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       issue(c + 1);
       if (wave_scores) {
         const f32x16 acc = chunk_scores(c & 1);
-        float t[16];
-        float cm = -INFINITY;
+        const int lim = (c + 1) * ROWS <= p.k_tiles ? ROWS : p.k_tiles - c * ROWS;  // valid key tiles
+        auto masked_max = [&]() {
+          float cm = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const bool kv = c * ROWS + acc_row(r, hl) < p.k_tiles;
-          t[r] = kv ? acc[r] * p.scale_log2 : -INFINITY;
-          cm = fmaxf(cm, t[r]);
-        }
-        const float mn = fmaxf(m, cm);
-        if (mn > -INFINITY) {
+          for (int r = 0; r < 16; ++r)
+            if (acc_row(r, hl) < lim) cm = fmaxf(cm, acc[r] * p.scale_log2);
+          return cm;
+        };
+        auto exp_sum = [&](float ref) {
           float sum = 0.f;
+          if (lim == ROWS) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) sum += exp2_fast(t[r] - mn);
-          z = (m > -INFINITY ? z * exp2_fast(m - mn) : 0.f) + sum;
-          m = mn;
+            for (int r = 0; r < 16; ++r) sum += exp2_fast(fmaf(acc[r], p.scale_log2, -ref));
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (acc_row(r, hl) < lim) sum += exp2_fast(fmaf(acc[r], p.scale_log2, -ref));
+          }
+          return sum;
+        };
+        if (!(m > -INFINITY)) m = masked_max();  // the tile's first chunk (stays -inf without valid keys)
+        if (m > -INFINITY) {
+          float sum = exp_sum(m);
+          if (!(sum <= 0x1p64f)) {  // a logit far above the reference: move it to this chunk's maximum
+            const float mn = fmaxf(m, masked_max());
+            z *= exp2_fast(m - mn);
+            m = mn;
+            sum = exp_sum(m);
+          }
+          z += sum;
         }
       }
     }
@@ -397,16 +417,22 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       if (!wave_scores) continue;
       const f32x16 acc = chunk_scores(step & 1);
       float pr[16];
+      if ((c + 1) * ROWS <= p.k_tiles) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const bool kv = c * ROWS + acc_row(r, hl) < p.k_tiles;
-        pr[r] = kv ? exp2_fast(acc[r] * p.scale_log2 - M) * invZ : 0.f;
+        for (int r = 0; r < 16; ++r) pr[r] = exp2_fast(fmaf(acc[r], p.scale_log2, -M));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          pr[r] = c * ROWS + acc_row(r, hl) < p.k_tiles ? exp2_fast(fmaf(acc[r], p.scale_log2, -M)) : 0.f;
       }
+      // exp2(s - M) summed over a query tile's key tiles of the block, scaled
+      // by that tile's 1/Z, then summed over the block's query tiles
       if constexpr (TPB == 8) {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           float sum = (pr[4 * b] + pr[4 * b + 1]) + (pr[4 * b + 2] + pr[4 * b + 3]);
           sum += __shfl_xor(sum, 32);
+          sum *= invZ;
           sum += __shfl_xor(sum, 1);
           sum += __shfl_xor(sum, 2);
           sum += __shfl_xor(sum, 4);
@@ -416,7 +442,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       } else {
 #pragma unroll
         for (int gg = 0; gg < 4; ++gg) {
-          float sum = (pr[4 * gg] + pr[4 * gg + 1]) + (pr[4 * gg + 2] + pr[4 * gg + 3]);
+          float sum = ((pr[4 * gg] + pr[4 * gg + 1]) + (pr[4 * gg + 2] + pr[4 * gg + 3])) * invZ;
           sum += __shfl_xor(sum, 1);
           sum += __shfl_xor(sum, 2);
           const int kbk = c * 8 + 2 * gg + hl;
