@@ -248,6 +248,37 @@ def hilbert3d_perm(f: int, h: int, w: int) -> torch.Tensor:
     return out
 
 
+def _norm_rope_call(entry: str, x: torch.Tensor, out: torch.Tensor, weight: Optional[torch.Tensor], eps: float,
+                    cos: Optional[torch.Tensor], sin: Optional[torch.Tensor], rope_param: int,
+                    weight_len: int, table_shape: Tuple[int, int]) -> None:
+    _require_device(x, out, weight, cos, sin)
+    if x.dim() != 4 or out.shape != x.shape:
+        raise ValueError(f"{entry}: x and out must be 4-D [B, L, H, D] of one shape, got "
+                         f"{tuple(x.shape)} and {tuple(out.shape)}")
+    if x.dtype not in (torch.bfloat16, torch.float16) or out.dtype != x.dtype:
+        raise ValueError(f"{entry}: x and out must both be bf16 or f16, got {x.dtype} and {out.dtype}")
+    if x.stride(3) != 1 or out.stride(3) != 1:
+        raise ValueError(f"{entry}: the channel (last) stride must be 1")
+    B, L, H, D = x.shape
+    w_code = 0
+    if weight is not None:
+        if weight.dim() != 1 or weight.numel() != weight_len or not weight.is_contiguous():
+            raise ValueError(f"{entry}: weight must be a contiguous [{weight_len}] vector")
+        if weight.dtype not in DTYPE_CODE:
+            raise ValueError(f"{entry}: weight dtype {weight.dtype} is not supported")
+        w_code = DTYPE_CODE[weight.dtype]
+    if (cos is None) != (sin is None):
+        raise ValueError(f"{entry}: pass both cos and sin or neither")
+    if cos is not None:
+        for name, t in (("cos", cos), ("sin", sin)):
+            if t.dtype != torch.float32 or tuple(t.shape) != table_shape or not t.is_contiguous():
+                raise ValueError(f"{entry}: {name} must be contiguous float32 {table_shape}, got "
+                                 f"{t.dtype} {tuple(t.shape)}")
+    _lib.call(entry, _ptr(x), x.stride(0), x.stride(1), x.stride(2), _ptr(out), out.stride(0),
+              out.stride(1), out.stride(2), B, L, H, D, DTYPE_CODE[x.dtype], _ptr(weight), w_code, float(eps),
+              _ptr(cos), _ptr(sin), int(rope_param), _stream(x))
+
+
 def norm_rope(x: torch.Tensor, out: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
               cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None, rope_skip: int = 0) -> None:
     """RMSNorm over the H*D channels of each token and/or complex RoPE of each
@@ -255,33 +286,30 @@ def norm_rope(x: torch.Tensor, out: torch.Tensor, weight: Optional[torch.Tensor]
     stride 1 (any other strides, e.g. a [B, H, L, D] tensor permuted to
     (0, 2, 1, 3)); x and out may be the same tensor. weight None skips the
     norm, cos/sin None (fp32 [L - rope_skip, D/2]) skip the rotation."""
-    _require_device(x, out, weight, cos, sin)
-    if x.dim() != 4 or out.shape != x.shape:
-        raise ValueError(f"norm_rope: x and out must be 4-D [B, L, H, D] of one shape, got "
-                         f"{tuple(x.shape)} and {tuple(out.shape)}")
-    if x.dtype not in (torch.bfloat16, torch.float16) or out.dtype != x.dtype:
-        raise ValueError(f"norm_rope: x and out must both be bf16 or f16, got {x.dtype} and {out.dtype}")
-    if x.stride(3) != 1 or out.stride(3) != 1:
-        raise ValueError("norm_rope: the channel (last) stride must be 1")
-    B, L, H, D = x.shape
-    w_code = 0
-    if weight is not None:
-        if weight.dim() != 1 or weight.numel() != H * D or not weight.is_contiguous():
-            raise ValueError(f"norm_rope: weight must be a contiguous [{H * D}] vector")
-        if weight.dtype not in DTYPE_CODE:
-            raise ValueError(f"norm_rope: weight dtype {weight.dtype} is not supported")
-        w_code = DTYPE_CODE[weight.dtype]
-    if (cos is None) != (sin is None):
-        raise ValueError("norm_rope: pass both cos and sin or neither")
-    if cos is not None:
-        want = (L - rope_skip, D // 2)
-        for name, t in (("cos", cos), ("sin", sin)):
-            if t.dtype != torch.float32 or tuple(t.shape) != want or not t.is_contiguous():
-                raise ValueError(f"norm_rope: {name} must be contiguous float32 {want}, got "
-                                 f"{t.dtype} {tuple(t.shape)}")
-    _lib.call("dfs_norm_rope", _ptr(x), x.stride(0), x.stride(1), x.stride(2), _ptr(out), out.stride(0),
-              out.stride(1), out.stride(2), B, L, H, D, DTYPE_CODE[x.dtype], _ptr(weight), w_code, float(eps),
-              _ptr(cos), _ptr(sin), int(rope_skip), _stream(x))
+    L, H, D = x.shape[1:4] if x.dim() == 4 else (0, 0, 0)
+    _norm_rope_call("dfs_norm_rope", x, out, weight, eps, cos, sin, rope_skip, H * D, (L - rope_skip, D // 2))
+
+
+def head_norm_rope(x: torch.Tensor, out: torch.Tensor, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                   cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                   rope_rows: Optional[int] = None) -> None:
+    """The HunyuanVideo form: RMSNorm of each head's D channels (weight [D])
+    and real RoPE with fp32 tables [rope_rows, D] on tokens l < rope_rows
+    (default: all); same views as norm_rope."""
+    L, H, D = x.shape[1:4] if x.dim() == 4 else (0, 0, 0)
+    rows = L if rope_rows is None else int(rope_rows)
+    _norm_rope_call("dfs_head_norm_rope", x, out, weight, eps, cos, sin, rows, D, (rows, D))
+
+
+def _split_heads(fn, x: torch.Tensor, heads: int, *args) -> torch.Tensor:
+    if x.dim() != 3 or x.shape[-1] % heads:
+        raise ValueError(f"expected [B, L, H*D] with H = {heads}, got {tuple(x.shape)}")
+    B, L, C = x.shape
+    D = C // heads
+    src = x if x.stride(2) == 1 else x.contiguous()
+    out = torch.empty((B, heads, L, D), dtype=x.dtype, device=x.device)
+    fn(src.unflatten(2, (heads, D)), out.permute(0, 2, 1, 3), *args)
+    return out
 
 
 def norm_rope_heads(x: torch.Tensor, heads: int, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
@@ -289,12 +317,11 @@ def norm_rope_heads(x: torch.Tensor, heads: int, weight: Optional[torch.Tensor] 
                     rope_skip: int = 0) -> torch.Tensor:
     """Projection output [B, L, H*D] -> new [B, H, L, D] tensor, normalised
     and rotated on the way (the head split of the attention inputs)."""
-    if x.dim() != 3 or x.shape[-1] % heads:
-        raise ValueError(f"norm_rope_heads: expected [B, L, H*D] with H = {heads}, got {tuple(x.shape)}")
-    B, L, C = x.shape
-    D = C // heads
-    src = x if x.stride(2) == 1 else x.contiguous()
-    out = torch.empty((B, heads, L, D), dtype=x.dtype, device=x.device)
-    norm_rope(src.view(B, L, heads, D) if src.is_contiguous() else src.unflatten(2, (heads, D)),
-              out.permute(0, 2, 1, 3), weight, eps, cos, sin, rope_skip)
-    return out
+    return _split_heads(norm_rope, x, heads, weight, eps, cos, sin, rope_skip)
+
+
+def head_norm_rope_heads(x: torch.Tensor, heads: int, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                         cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                         rope_rows: Optional[int] = None) -> torch.Tensor:
+    """norm_rope_heads with the per-head norm and real RoPE of head_norm_rope."""
+    return _split_heads(head_norm_rope, x, heads, weight, eps, cos, sin, rope_rows)

@@ -24,6 +24,7 @@ import torch.nn.functional as F
 
 from .attention_hyvideo import DFS_Attention, dfs_attention
 from .fullattention import full_attention
+from .replace_wan import rms_norm_like
 from .utils.logger import logger
 
 
@@ -43,6 +44,30 @@ def apply_rotary_emb(x: torch.Tensor, freqs_cis: Tuple[torch.Tensor, torch.Tenso
     xr, xi = x.reshape(*x.shape[:-1], -1, 2).unbind(-1)
     rotated = torch.stack([-xi, xr], dim=-1).flatten(3)
     return (x.float() * cos + rotated.float() * sin).to(x.dtype)
+
+
+def fused_qkv_heads_per_head(attn, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                             image_rotary_emb, rope_rows: int):
+    """[B, L, H*D] projections -> [B, H, L, D] q, k, v in the library's fused
+    kernel: per-head RMSNorm (attn.norm_q / norm_k over D) and real RoPE of
+    the first rope_rows tokens of q and k (the text after them is not
+    rotated), where the reference runs its RMSNorm and RoPE kernels
+    (replace_hyvideo.py:252-268)."""
+    from .ops import head_norm_rope_heads
+    from .replace_wan import _norm_args
+
+    heads = attn.heads
+    d = query.shape[-1] // heads
+    cos = sin = None
+    if image_rotary_emb is not None:
+        cos, sin = (t.to(device=query.device, dtype=torch.float32).reshape(-1, d).contiguous()
+                    for t in image_rotary_emb)
+    wq, eq = _norm_args(attn.norm_q, d, query)
+    wk, ek = _norm_args(attn.norm_k, d, key)
+    q = head_norm_rope_heads(query, heads, wq, eq, cos, sin, rope_rows)
+    k = head_norm_rope_heads(key, heads, wk, ek, cos, sin, rope_rows)
+    v = head_norm_rope_heads(value, heads)
+    return q, k, v
 
 
 class HunyuanVideo_DFSAttn_Processor2_0:
@@ -167,14 +192,11 @@ class HunyuanVideo_DFSAttn_Processor2_0:
         os.replace(summary_path + ".tmp", summary_path)
         logger.info(f"Attention debug dump saved to {tensor_path}")
 
-    def __call__(self, attn, hidden_states: torch.Tensor, encoder_hidden_states: Optional[torch.Tensor] = None,
-                 attention_mask: Optional[torch.Tensor] = None, image_rotary_emb=None):
-        single_stream = attn.add_q_proj is None and encoder_hidden_states is not None
-        if single_stream:
-            hidden_states = torch.cat([hidden_states, encoder_hidden_states], dim=1)
-        query = attn.to_q(hidden_states)
-        key = attn.to_k(hidden_states)
-        value = attn.to_v(hidden_states)
+    @staticmethod
+    def _torch_qkv_heads(attn, query, key, value, image_rotary_emb, text: Optional[torch.Tensor]):
+        """Head split, the model's QK norm modules and diffusers-style RoPE in
+        torch (the reference's fallback, replace_hyvideo.py:247-290); with
+        ``text`` the RoPE covers the video tokens before it."""
         query = query.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
         key = key.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
         value = value.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()
@@ -183,8 +205,8 @@ class HunyuanVideo_DFSAttn_Processor2_0:
         if attn.norm_k is not None:
             key = attn.norm_k(key)
         if image_rotary_emb is not None:
-            if single_stream:  # RoPE on the video part only; text follows the video
-                n_text = encoder_hidden_states.shape[1]
+            if text is not None:  # RoPE on the video part only; text follows the video
+                n_text = text.shape[1]
                 query = torch.cat([apply_rotary_emb(query[:, :, :-n_text], image_rotary_emb),
                                    query[:, :, -n_text:]], dim=2)
                 key = torch.cat([apply_rotary_emb(key[:, :, :-n_text], image_rotary_emb),
@@ -192,6 +214,27 @@ class HunyuanVideo_DFSAttn_Processor2_0:
             else:
                 query = apply_rotary_emb(query, image_rotary_emb)
                 key = apply_rotary_emb(key, image_rotary_emb)
+        return query, key, value
+
+    def __call__(self, attn, hidden_states: torch.Tensor, encoder_hidden_states: Optional[torch.Tensor] = None,
+                 attention_mask: Optional[torch.Tensor] = None, image_rotary_emb=None):
+        single_stream = attn.add_q_proj is None and encoder_hidden_states is not None
+        if single_stream:
+            hidden_states = torch.cat([hidden_states, encoder_hidden_states], dim=1)
+        query = attn.to_q(hidden_states)
+        key = attn.to_k(hidden_states)
+        value = attn.to_v(hidden_states)
+        head_dim = query.shape[-1] // attn.heads
+        if (self.mode != "flash" and query.is_cuda and head_dim % 8 == 0 and head_dim <= 512
+                and head_dim & (head_dim - 1) == 0 and query.shape[-1] <= 8192
+                and rms_norm_like(attn.norm_q, head_dim) and rms_norm_like(attn.norm_k, head_dim)):
+            # fused per-head QK-RMSNorm + RoPE + head split on the GPU, where
+            # the reference runs its fast kernels (replace_hyvideo.py:252-268)
+            rope_rows = query.shape[1] - (encoder_hidden_states.shape[1] if single_stream else 0)
+            query, key, value = fused_qkv_heads_per_head(attn, query, key, value, image_rotary_emb, rope_rows)
+        else:
+            query, key, value = self._torch_qkv_heads(attn, query, key, value, image_rotary_emb,
+                                                      encoder_hidden_states if single_stream else None)
         if attn.add_q_proj is not None and encoder_hidden_states is not None:  # double stream
             eq = attn.add_q_proj(encoder_hidden_states).unflatten(2, (attn.heads, -1)).transpose(1, 2)
             ek = attn.add_k_proj(encoder_hidden_states).unflatten(2, (attn.heads, -1)).transpose(1, 2)

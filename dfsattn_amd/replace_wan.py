@@ -43,6 +43,17 @@ def rope_tables(rotary_emb: torch.Tensor):
     return f.real.to(torch.float32).contiguous(), f.imag.to(torch.float32).contiguous()
 
 
+def rms_norm_like(norm, channels: int) -> bool:
+    """True for None or an RMSNorm-style module (eps, optional [channels]
+    scale, no bias) that the fused kernels can apply."""
+    if norm is None:
+        return True
+    if isinstance(norm, torch.nn.LayerNorm) or getattr(norm, "bias", None) is not None or not hasattr(norm, "eps"):
+        return False
+    weight = getattr(norm, "weight", None)
+    return weight is None or (weight.dim() == 1 and weight.numel() == channels)
+
+
 def _norm_args(norm, channels: int, x: torch.Tensor):
     """(weight, eps) of an RMSNorm module for the fused kernel (None: no norm)."""
     if norm is None:
@@ -142,7 +153,9 @@ class Wan_DFSAttn_Processor2_0:
         query = attn.to_q(hidden_states)
         key = attn.to_k(encoder_hidden_states)
         value = attn.to_v(encoder_hidden_states)
-        if self.mode != "flash" and query.is_cuda:
+        if (self.mode != "flash" and query.is_cuda and query.shape[-1] <= 8192
+                and (query.shape[-1] // attn.heads) % 8 == 0 and rms_norm_like(attn.norm_q, query.shape[-1])
+                and rms_norm_like(attn.norm_k, key.shape[-1])):
             # fused QK-RMSNorm + RoPE + head split on the GPU, where the
             # reference runs its RMSNorm and RoPE kernels (replace_wan.py:159-205)
             query, key, value = fused_qkv_heads(attn, query, key, value, rotary_emb)

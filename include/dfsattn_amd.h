@@ -214,6 +214,28 @@ int dfs_norm_rope(const void* x, int64_t x_sb, int64_t x_sl, int64_t x_sh,
                   const float* sin_table, int64_t rope_skip,
                   dfs_stream_t stream);
 
+/*
+ * The HunyuanVideo form of the above (same layouts and strides):
+ *   - weight != NULL: RMSNorm of each head's D channels (weight [D]),
+ *     replacing the reference's rms_norm_forward (kernels/csrc/ops.h:52-75)
+ *     as applied per head by apply_qk_norm (kernels/__init__.py), called at
+ *     replace_hyvideo.py:252-253. D a power of two <= 512.
+ *   - cos/sin != NULL: fp32 tables [rope_rows][D]; token l < rope_rows has
+ *     each (even, odd) channel pair rotated, out[2i] = x[2i]*cos[2i] -
+ *     x[2i+1]*sin[2i], out[2i+1] = x[2i+1]*cos[2i+1] + x[2i]*sin[2i+1], every
+ *     product and sum rounded in fp32; the text rows after rope_rows are not
+ *     rotated. Replaces apply_qk_rope_inplace_cossin_txtlast
+ *     (kernels/csrc/ops.h:146-205) as called by apply_qk_rope_single/double
+ *     (replace_hyvideo.py:262-268).
+ */
+int dfs_head_norm_rope(const void* x, int64_t x_sb, int64_t x_sl, int64_t x_sh,
+                       void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh,
+                       int64_t batch, int64_t seq_len, int64_t heads,
+                       int64_t head_dim, int dtype, const void* weight,
+                       int weight_dtype, float eps, const float* cos_table,
+                       const float* sin_table, int64_t rope_rows,
+                       dfs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,10 @@ Each function restates the reference (``codesiena/DFSattn``) at the cited
   product through ``torch.view_as_complex`` (replace_wan.py:209-213), and by
   the rotation invariants (angle 0 is the identity, pair norms are kept,
   rotating by -angle undoes +angle).
+* ``rope_real_pairs`` (rope_enc_txtlast.cuh; replace_hyvideo.py:271-290):
+  pinned within fp32 rounding against the float64 complex rotation of the
+  same angles (tables repeat each angle over a pair), and by the rotation
+  invariants; ``head_rmsnorm`` reduces to ``rmsnorm_rows`` over one head.
 """
 from __future__ import annotations
 
@@ -516,4 +520,39 @@ def norm_rope_heads(x: torch.Tensor, heads: int, weight: Optional[torch.Tensor] 
     if cos is not None:
         y = y.clone()
         y[:, :, rope_skip:] = rope_complex_pairs(y[:, :, rope_skip:], cos, sin)
+    return y
+
+
+def head_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm of each head's D channels (last axis) as the reference's
+    narrow RMSNorm kernel (kernels/include/norm/narrow_rms_norm.cuh): fp32
+    sum of squares, (x * rstd) * w, stored in x's dtype."""
+    return rmsnorm_rows(x, weight, eps)
+
+
+def rope_real_pairs(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Real RoPE of adjacent channel pairs with fp32 tables [L, D]
+    (rope_enc_txtlast.cuh; the torch fallback at replace_hyvideo.py:271-290):
+    out[2i] = x[2i] cos[2i] - x[2i+1] sin[2i], out[2i+1] = x[2i+1] cos[2i+1] +
+    x[2i] sin[2i+1], every product and sum rounded in fp32."""
+    xf = x.float()
+    xe, xo = xf[..., 0::2], xf[..., 1::2]
+    ce, co = cos[..., 0::2], cos[..., 1::2]
+    se, so = sin[..., 0::2], sin[..., 1::2]
+    out = torch.stack([xe * ce + (-xo) * se, xo * co + xe * so], dim=-1).flatten(-2)
+    return out.to(x.dtype)
+
+
+def head_norm_rope_heads(x: torch.Tensor, heads: int, weight: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                         cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                         rope_rows: Optional[int] = None) -> torch.Tensor:
+    """[B, L, H*D] -> [B, H, L, D]: head split, per-head RMSNorm (if weight),
+    real RoPE of tokens l < rope_rows (if cos; default all) by table row l."""
+    y = x.unflatten(-1, (heads, -1)).transpose(1, 2).contiguous()
+    if weight is not None:
+        y = head_rmsnorm(y, weight, eps)
+    if cos is not None:
+        rows = y.shape[2] if rope_rows is None else rope_rows
+        y = y.clone()
+        y[:, :, :rows] = rope_real_pairs(y[:, :, :rows], cos, sin)
     return y

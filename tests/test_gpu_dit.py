@@ -77,6 +77,70 @@ def test_norm_rope_heads_matches_oracle(dev, B, L, H, D, dtype, wdt, rope, skip)
     assert bool(((got.float() - r).abs() <= tol).all())
 
 
+HEAD_CASES = [
+    # B, L, H, D, dtype, weight dtype (None: no norm), rope, rope_rows
+    (1, 300, 24, 128, torch.bfloat16, torch.bfloat16, True, 256),  # text rows after 256
+    (2, 77, 3, 64, torch.float16, torch.float32, True, 77),
+    (1, 50, 24, 128, torch.bfloat16, None, True, 40),  # RoPE only
+    (1, 33, 4, 128, torch.bfloat16, torch.bfloat16, False, 0),  # norm only
+]
+
+
+@pytest.mark.parametrize("B,L,H,D,dtype,wdt,rope,rows", HEAD_CASES)
+def test_head_norm_rope_matches_oracle(dev, B, L, H, D, dtype, wdt, rope, rows):
+    """The HunyuanVideo form: per-head RMSNorm and real RoPE on the first
+    `rows` tokens."""
+    from dfsattn_amd import ops
+    print(f"head_norm_rope B={B} L={L} H={H} D={D} {dtype} w={wdt} rope={rope} rows={rows}", flush=True)
+    g = torch.Generator().manual_seed(L * H + D + 1)
+    x = (torch.randn(B, L, H * D, generator=g) * 3).to(dtype)
+    w = None if wdt is None else (torch.rand(D, generator=g) + 0.5).to(wdt)
+    cos = sin = None
+    if rope:
+        ang = (torch.rand(rows, D // 2, generator=g, dtype=torch.float64) * 50).repeat_interleave(2, dim=-1)
+        cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    ref = orc.head_norm_rope_heads(x, H, w, 1e-6, cos, sin, rows if rope else None)
+    got = ops.head_norm_rope_heads(x.to(dev), H, None if w is None else w.to(dev), 1e-6,
+                                   None if cos is None else cos.to(dev), None if sin is None else sin.to(dev),
+                                   rows if rope else None).cpu()
+    assert got.shape == (B, H, L, D) and got.dtype == dtype
+    if w is None:
+        assert torch.equal(got, ref)
+        return
+    assert float((got == ref).float().mean()) > 0.99
+    if not rope:
+        assert int(_ulps(got, ref).max()) <= 1
+        return
+    mant = 7 if dtype == torch.bfloat16 else 10
+    r = ref.float()
+    pair = torch.sqrt(r[..., 0::2] ** 2 + r[..., 1::2] ** 2).repeat_interleave(2, dim=-1)
+    assert bool(((got.float() - r).abs() <= 2.0 ** -mant * (pair + r.abs()) + 1e-6).all())
+
+
+@torch.no_grad()
+def test_hunyuan_fused_qkv_matches_torch_path(dev):
+    """The Hunyuan processor's fused per-head norm + RoPE against its torch
+    path (model norm modules, diffusers-style RoPE) on a single-stream call
+    with text after the video."""
+    from stubs import StubAttention
+    from dfsattn_amd.replace_hyvideo import HunyuanVideo_DFSAttn_Processor2_0, fused_qkv_heads_per_head
+    torch.manual_seed(4)
+    attn = StubAttention(dim=256, heads=2, norm_shape=128).to(dev, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(9)
+    n_video, n_text = 300, 40
+    x = torch.randn(1, n_video + n_text, 256, generator=g).to(dev, torch.bfloat16)
+    text = x[:, n_video:]
+    ang = (torch.rand(n_video, 64, generator=g, dtype=torch.float64) * 20).repeat_interleave(2, dim=-1)
+    rope = (torch.cos(ang).float().to(dev), torch.sin(ang).float().to(dev))
+    ql, kl, vl = attn.to_q(x), attn.to_k(x), attn.to_v(x)
+    fq, fk, fv = fused_qkv_heads_per_head(attn, ql, kl, vl, rope, n_video)
+    tq, tk, tv = HunyuanVideo_DFSAttn_Processor2_0._torch_qkv_heads(attn, ql, kl, vl, rope, text)
+    assert torch.equal(fv, tv)
+    for f, t in ((fq, tq), (fk, tk)):
+        assert _rel(f.cpu(), t.cpu()) < 5e-3
+        assert float((f.float() - t.float()).abs().max()) < 0.1
+
+
 def test_norm_rope_in_place_on_attention_layout(dev):
     """RoPE in place on a [B, H, S, D] tensor (the layout of the reference's
     apply_qk_rope_inplace_cossin_complex) with a skipped prefix."""

@@ -273,3 +273,33 @@ def test_norm_rope_heads_oracle_layout():
             head = normed[b, :, h * 16:(h + 1) * 16]
             assert torch.equal(out[b, h, :3], head[:3])  # rows before rope_skip are not rotated
             assert torch.equal(out[b, h, 3:], orc.rope_complex_pairs(head[3:], cos, sin))
+
+
+def test_real_rope_oracle_against_complex_rotation():
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(2, 3, 40, 64, generator=g)
+    ang = torch.rand(40, 32, generator=g, dtype=torch.float64) * 30
+    # real tables repeat each angle over its (even, odd) pair
+    cos = torch.cos(ang).float().repeat_interleave(2, dim=-1)
+    sin = torch.sin(ang).float().repeat_interleave(2, dim=-1)
+    got = orc.rope_real_pairs(x, cos, sin)
+    freqs = torch.complex(torch.cos(ang).float().double(), torch.sin(ang).float().double())
+    ref = torch.view_as_real(torch.view_as_complex(x.double().unflatten(-1, (-1, 2))) * freqs).flatten(-2)
+    torch.testing.assert_close(got.double(), ref, rtol=1e-6, atol=1e-6)
+    assert torch.equal(orc.rope_real_pairs(x, torch.ones(40, 64), torch.zeros(40, 64)), x)
+    back = orc.rope_real_pairs(got, cos, -sin)
+    torch.testing.assert_close(back, x, rtol=1e-5, atol=1e-5)
+    quarter = orc.rope_real_pairs(x[..., :1, :], torch.zeros(1, 64), torch.ones(1, 64))
+    assert torch.equal(quarter[..., 0::2], -x[..., :1, 1::2]) and torch.equal(quarter[..., 1::2], x[..., :1, 0::2])
+
+
+def test_head_norm_rope_oracle_layout():
+    g = torch.Generator().manual_seed(15)
+    x = torch.randn(1, 10, 2 * 16, generator=g).bfloat16()
+    w = torch.rand(16, generator=g) + 0.5
+    cos, sin = torch.rand(7, 16, generator=g), torch.rand(7, 16, generator=g)
+    out = orc.head_norm_rope_heads(x, 2, w, 1e-6, cos, sin, rope_rows=7)
+    for h in range(2):
+        head = orc.rmsnorm_rows(x[0, :, h * 16:(h + 1) * 16], w, 1e-6)  # each head normalised alone
+        assert torch.equal(out[0, h, :7], orc.rope_real_pairs(head[:7], cos, sin))
+        assert torch.equal(out[0, h, 7:], head[7:])  # text rows after rope_rows are not rotated
