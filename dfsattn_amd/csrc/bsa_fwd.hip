@@ -97,17 +97,19 @@ __device__ __forceinline__ float xhalf_sum(float v) {
 // (head, query block) of this workgroup; false for a padding slot.
 // Hardware deals workgroup b to XCD b % 8 and each XCD runs its workgroups in
 // increasing b. Head-major mode (default): the i-th workgroup of XCD x takes
-// head i / S and query block x * S + i % S (S = ceil(Qb / 8)), so all eight
-// XCDs sweep the same head together: one head's K/V (38.7 MB at 75.6k tokens)
-// stays resident in the shared last-level cache while each XCD's L2 serves
-// neighbouring query blocks. Mode 1: each XCD owns a contiguous run of
+// head h = i / S and query block ((x + h) % 8) * S + i % S (S = ceil(Qb / 8)),
+// so all eight XCDs sweep the same head together: one head's K/V (38.7 MB at
+// 75.6k tokens) stays resident in the shared last-level cache while each
+// XCD's L2 serves neighbouring query blocks. The range an XCD takes rotates
+// with the head, so rows of unequal length (HunyuanVideo's dense text rows
+// at the end of every head) spread over all XCDs instead of one. Mode 1: each XCD owns a contiguous run of
 // (head, query block) pairs instead.
 __device__ __forceinline__ bool wg_coords(const BsaParams& p, int& h, int& qb) {
   const int b = blockIdx.x, xcd = b & 7, i = b >> 3;
   if (p.sched == 0) {
     const int S = (p.Qb + 7) >> 3;
     h = i / S;
-    qb = xcd * S + (i - h * S);
+    qb = ((xcd + h) & 7) * S + (i - h * S);
     return qb < p.Qb;
   }
   const int nwg = gridDim.x, per = nwg >> 3, rem = nwg & 7;
@@ -588,7 +590,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
 }
 
 // (head, pair of query blocks) of an eight-wave workgroup; head-major across
-// XCDs like wg_coords.
+// XCDs with the per-head rotation of wg_coords.
 
 template <int G>
 __device__ __forceinline__ bool group_coords(const BsaParams& p, int& h, int& grp) {
@@ -596,7 +598,7 @@ __device__ __forceinline__ bool group_coords(const BsaParams& p, int& h, int& gr
   const int b = blockIdx.x, xcd = b & 7, i = b >> 3;
   const int S = (groups + 7) >> 3;
   h = i / S;
-  grp = xcd * S + (i - h * S);
+  grp = ((xcd + h) & 7) * S + (i - h * S);
   return grp < groups;
 }
 
