@@ -16,6 +16,7 @@ import torch
 
 from . import ops
 from .layout import ScoringLayout, TopkPolicy
+from .utils.logger import logger
 
 SUPPORTED_EXECUTION = "native"
 
@@ -72,6 +73,20 @@ class DfsCore:
     ``_policy`` and the class-level state dictionaries."""
 
     operand_dtype: Optional[torch.dtype] = None  # None -> operand_dtype_for default
+    # True: f16 operands are checked for values beyond the f16 range (one
+    # device-to-host read per call) and the call is redone on bf16 operands
+    # when any is found; False (default) keeps the call free of host syncs.
+    check_overflow: bool = False
+
+    def _prepare(self, q, k, v, perm, layout, pool: bool) -> "ops.Prepared":
+        od = operand_dtype_for(q.dtype, self.operand_dtype)
+        if self.check_overflow and od == torch.float16 and q.dtype == torch.bfloat16:
+            prep = ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=od, pool=pool, check_overflow=True)
+            if int(prep.overflow.item()):
+                logger.warning("DFS attention inputs exceed the f16 range; running this call on bf16 operands")
+                prep = ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=torch.bfloat16, pool=pool)
+            return prep
+        return ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=od, pool=pool)
 
     # --- permutation -----------------------------------------------------
     def _device_permutation(self, seq_len: int, device: torch.device) -> torch.Tensor:
@@ -166,8 +181,7 @@ class DfsCore:
             seg_perm = perm[start:end] - start if start else perm[:end]
             q_s, k_s, v_s = (x[:, :, start:end] for x in (q, k, v))
             lay = ScoringLayout(n, n, 16, self.block_size)
-            prep = ops.prepare_qkv(q_s, k_s, v_s, seg_perm.contiguous(), lay,
-                                   operand_dtype=operand_dtype_for(q.dtype, self.operand_dtype), pool=False)
+            prep = self._prepare(q_s, k_s, v_s, seg_perm.contiguous(), lay, pool=False)
             outs.append(ops.bsa_fwd(prep, row_ptr, col_idx, scale=None, out_dtype=prep.dtype,
                                     out_perm=seg_perm.contiguous()))
         return torch.cat(outs, dim=2)
@@ -208,7 +222,7 @@ class DfsCore:
         recompute = entry is None or self.cache_flag
         rec = cls.timing_recorder
         t_perm = rec.start(device)
-        prep = ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=operand_dtype_for(q.dtype, self.operand_dtype), pool=recompute)
+        prep = self._prepare(q, k, v, perm, layout, pool=recompute)
         rec.stop(t_perm, phase="qkv_permute", step_idx=self.step_idx, layer_idx=self.layer_idx, device=device)
         if recompute:
             t_topk = rec.start(device)

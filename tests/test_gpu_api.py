@@ -223,3 +223,29 @@ def test_records_and_mask_export_from_a_call(dev, tmp_path):
         DFS_Attention.configure_mask_export(None)
         DFS_Attention.set_record_timing(False)
         DFS_Attention.set_record_density(False)
+
+
+def test_overflow_check_reruns_on_bf16_operands(dev):
+    """V values beyond the f16 range: with DFS_Attention.check_overflow the
+    call is redone on bf16 operands and matches the fp32 oracle; the
+    default f16 path is documented to need inputs inside the f16 range."""
+    from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[0]
+    q, k, v = synth_qkv(cfg, dtype=torch.bfloat16)
+    v = v.clone()
+    v[:, :, 100, :] = 2.0e5  # bf16 holds it, f16 (max 65504) does not
+    perm = hilbert3d_perm(*cfg.grid)
+    DFS_Attention.check_overflow = True
+    try:
+        out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=24, skip_steps=12, cache_interval=12,
+                            layer_idx=5, sparsity=0.3, sparsity_dcrt=0.1, tile_size=16, video_perm=perm)
+    finally:
+        DFS_Attention.check_overflow = False
+    assert bool(torch.isfinite(out).all())
+    mask = DFS_Attention._cached_metadata[(5, "native", 128, 16, 16)]["block_mask"].cpu()
+    p, inv = orc.full_permutation(perm, q.shape[2])
+    ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
+    assert _rel(out.cpu(), ref) < 6e-3  # bf16 operands and output
