@@ -16,13 +16,17 @@
 //    waves of 32 query rows walking the row's kept key blocks; two
 //    workgroups per CU, single K and V buffers, the K copy of the next block
 //    overlapping softmax and PV, the V copy overlapping the next QK^T; the
-//    other workgroup on the CU fills the gaps.
+//    other workgroup on the CU fills the gaps. With f16 operands the row's
+//    reference maximum comes from its first block and later blocks skip the
+//    maximum (a block is redone only if its P overflows f16); the LDS operand
+//    reads run four MFMAs ahead, and the QK phase runs at raised wave
+//    priority.
 //  * ping-pong (DFSATTN_AMD_BSA_KERNEL=pp, f16 operands): one eight-wave
 //    workgroup per CU for two adjacent query blocks, the two four-wave groups
 //    alternating MFMA and softmax phases half a cycle apart (described at the
 //    kernel). It overlaps VALU with MFMA work but concentrates the LDS operand
-//    reads of a CU into its MFMA phases; at the 75.6k-token shape it runs about
-//    10% slower than split.
+//    reads of a CU into its MFMA phases; at the 75.6k-token shape it runs
+//    10-15% slower than split.
 //
 // LDS rows are 256 bytes; 16-byte chunk c of row r is stored at chunk
 // c ^ (r % 16) so the 32 rows read by one MFMA operand fetch hit distinct
