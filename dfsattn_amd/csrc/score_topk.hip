@@ -289,7 +289,10 @@ __global__ void __launch_bounds__(256) score_topk_kernel(ScoreParams p) {
 // (hi and lo) is copied once into LDS, double-buffered, for all four waves:
 // a quarter of the key traffic of one workgroup per 32 query tiles. The two
 // passes run as one stream of 2 * nchunks chunk steps with one barrier each.
-template <int D, int TPB>
+// GB (global block sums): the block sums go straight to scores_out (which
+// the caller provides) instead of LDS, so a workgroup needs only its key
+// chunks and the top-k histograms in LDS and four workgroups fit on a CU.
+template <int D, int TPB, bool GB>
 __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) {
   constexpr int CPR = D / 8;             // 16-byte chunks per pooled row
   constexpr int QBW = 32 / TPB;          // query blocks per wave
@@ -300,11 +303,11 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
   __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][2][TILE];  // [buffer][hi, lo]
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const Policy& pol = p.pol;
-  float* bsum = smem;                                          // [G][Kb]
-  uint32_t* hist = reinterpret_cast<uint32_t*>(bsum + G * pol.Kb);  // [4][256]
-
   const int h = blockIdx.y;
   const int qb0 = blockIdx.x * G;
+  // [G][Kb] block sums of this workgroup's query blocks
+  float* bsum = GB ? p.scores_out + (static_cast<int64_t>(h) * pol.scored_rows + qb0) * pol.Kb : smem;
+  uint32_t* hist = reinterpret_cast<uint32_t*>(GB ? smem : smem + G * pol.Kb);  // [4][256]
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int score_rows = p.scores_out ? pol.scored_rows : min(pol.scored_rows, pol.dense_row);
   const int qbw = qb0 + w * QBW;  // first query block of this wave
@@ -437,7 +440,9 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
           sum += __shfl_xor(sum, 2);
           sum += __shfl_xor(sum, 4);
           const int kbk = c * 4 + b;
-          if (hl == 0 && (l32 & 7) == 0 && kbk < pol.Kb) bsum[(w * QBW + (l32 >> 3)) * pol.Kb + kbk] = sum;
+          const int g = w * QBW + (l32 >> 3);
+          if (hl == 0 && (l32 & 7) == 0 && kbk < pol.Kb && (!GB || qb0 + g < pol.scored_rows))
+            bsum[g * pol.Kb + kbk] = sum;
         }
       } else {
 #pragma unroll
@@ -446,13 +451,14 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
           sum += __shfl_xor(sum, 1);
           sum += __shfl_xor(sum, 2);
           const int kbk = c * 8 + 2 * gg + hl;
-          if ((l32 & 3) == 0 && kbk < pol.Kb) bsum[(w * QBW + (l32 >> 2)) * pol.Kb + kbk] = sum;
+          const int g = w * QBW + (l32 >> 2);
+          if ((l32 & 3) == 0 && kbk < pol.Kb && (!GB || qb0 + g < pol.scored_rows)) bsum[g * pol.Kb + kbk] = sum;
         }
       }
     }
     wait_vmcnt_0();  // the trailing (empty) copies have retired
-    __syncthreads();
-    if (p.scores_out) {
+    __syncthreads();  // with GB: the block sums in global memory are visible to the workgroup
+    if (!GB && p.scores_out) {
       for (int i = tid; i < G * pol.Kb; i += 256) {
         const int g = i / pol.Kb, col = i - g * pol.Kb;
         const int qb = qb0 + g;
@@ -555,6 +561,8 @@ int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
   const size_t smem_wide = static_cast<size_t>(Gw) * k_blocks * sizeof(float) + 4 * 256 * 4;
   const size_t static_wide = 2 * 2 * 32 * static_cast<size_t>(head_dim) * 2;
   const bool wide = smem_wide + static_wide <= 160 * 1024;
+  const bool global_sums = scores_out != nullptr;  // block sums kept in scores_out, not LDS
+  const size_t smem_gb = 4 * 256 * 4;
   ScoreParams p{};
   p.q_hi = reinterpret_cast<const uint4*>(q_pool_hi);
   p.q_lo = reinterpret_cast<const uint4*>(q_pool_lo);
@@ -571,16 +579,28 @@ int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
   p.k_tiles = static_cast<int>(k_blocks * tpb);
   p.scale_log2 = static_cast<float>(1.4426950408889634 / sqrt(static_cast<double>(head_dim)));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (global_sums) {
+    dim3 grid(static_cast<unsigned>((q_blocks + Gw - 1) / Gw), static_cast<unsigned>(heads));
+    if (head_dim == 128 && tpb == 8)
+      score_topk_wide_kernel<128, 8, true><<<grid, 256, smem_gb, s>>>(p);
+    else if (head_dim == 128)
+      score_topk_wide_kernel<128, 4, true><<<grid, 256, smem_gb, s>>>(p);
+    else if (tpb == 8)
+      score_topk_wide_kernel<64, 8, true><<<grid, 256, smem_gb, s>>>(p);
+    else
+      score_topk_wide_kernel<64, 4, true><<<grid, 256, smem_gb, s>>>(p);
+    return check_launch(name);
+  }
   if (wide) {
     dim3 grid(static_cast<unsigned>((q_blocks + Gw - 1) / Gw), static_cast<unsigned>(heads));
     if (head_dim == 128 && tpb == 8)
-      score_topk_wide_kernel<128, 8><<<grid, 256, smem_wide, s>>>(p);
+      score_topk_wide_kernel<128, 8, false><<<grid, 256, smem_wide, s>>>(p);
     else if (head_dim == 128)
-      score_topk_wide_kernel<128, 4><<<grid, 256, smem_wide, s>>>(p);
+      score_topk_wide_kernel<128, 4, false><<<grid, 256, smem_wide, s>>>(p);
     else if (tpb == 8)
-      score_topk_wide_kernel<64, 8><<<grid, 256, smem_wide, s>>>(p);
+      score_topk_wide_kernel<64, 8, false><<<grid, 256, smem_wide, s>>>(p);
     else
-      score_topk_wide_kernel<64, 4><<<grid, 256, smem_wide, s>>>(p);
+      score_topk_wide_kernel<64, 4, false><<<grid, 256, smem_wide, s>>>(p);
     return check_launch(name);
   }
   dim3 grid(static_cast<unsigned>((q_blocks + G - 1) / G), static_cast<unsigned>(heads));

