@@ -36,6 +36,8 @@ SIGNATURES = {
                       _p, _i32, _f32, _p, _p, _i64, _p],
     "dfs_head_norm_rope": [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
                            _p, _i32, _f32, _p, _p, _i64, _p],
+    "dfs_adaln_modulate": [_p, _i64, _i64, _i32, _p, _p, _p, _p, _f32, _p, _p],
+    "dfs_gated_residual": [_p, _p, _p, _i64, _i64, _i32, _p, _p],
 }
 _RESTYPES = {"dfs_last_error": ctypes.c_char_p}
 ABI_VERSION = 1

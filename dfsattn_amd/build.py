@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 OUT_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_NAME = "libdfsattn_amd.so"
-SOURCES = ["host.cpp", "permute.hip", "score_topk.hip", "bsa_fwd.hip", "masks.hip", "norm_rope.hip"]
+SOURCES = ["host.cpp", "permute.hip", "score_topk.hip", "bsa_fwd.hip", "masks.hip", "norm_rope.hip", "dit_fused.hip"]
 ARCH = "gfx950"
 
 

@@ -327,3 +327,49 @@ def head_norm_rope_heads(x: torch.Tensor, heads: int, weight: Optional[torch.Ten
                          rope_rows: Optional[int] = None) -> torch.Tensor:
     """norm_rope_heads with the per-head norm and real RoPE of head_norm_rope."""
     return _split_heads(head_norm_rope, x, heads, weight, eps, cos, sin, rope_rows)
+
+
+def _vec(t: Optional[torch.Tensor], channels: int, name: str) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    v = t.reshape(-1)
+    if v.numel() != channels or v.dtype != torch.float32:
+        raise ValueError(f"{name} must hold {channels} float32 values, got {v.dtype} {tuple(t.shape)}")
+    return v.contiguous()
+
+
+def adaln_modulate(x: torch.Tensor, eps: float, weight: Optional[torch.Tensor] = None,
+                   bias: Optional[torch.Tensor] = None, scale: Optional[torch.Tensor] = None,
+                   shift: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """(LayerNorm(x) * weight + bias) * (1 + scale) + shift over the last
+    axis in fp32, returned in x's dtype; every vector is optional and holds
+    one fp32 value per channel (broadcast over the rows)."""
+    _require_device(x, weight, bias, scale, shift)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"adaln_modulate: x must be bf16 or f16, got {x.dtype}")
+    C = x.shape[-1]
+    vecs = [_vec(t, C, n) for t, n in ((weight, "weight"), (bias, "bias"), (scale, "scale"), (shift, "shift"))]
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    _lib.call("dfs_adaln_modulate", _ptr(xc), xc.numel() // C, C, DTYPE_CODE[x.dtype], *(_ptr(v) for v in vecs),
+              float(eps), _ptr(out), _stream(xc))
+    return out
+
+
+def gated_residual(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x + y * gate in fp32, returned in x's dtype (gate: one fp32 value per
+    channel); ``out`` may be x itself."""
+    _require_device(x, y, gate, out)
+    if x.dtype not in (torch.bfloat16, torch.float16) or y.dtype != x.dtype or y.shape != x.shape:
+        raise ValueError("gated_residual: x and y must be bf16 or f16 tensors of one shape and dtype")
+    C = x.shape[-1]
+    g = _vec(gate, C, "gate")
+    xc, yc = x.contiguous(), y.contiguous()
+    if out is None:
+        out = torch.empty_like(xc)
+    elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+        raise ValueError("gated_residual: out must be contiguous and shaped like x")
+    _lib.call("dfs_gated_residual", _ptr(xc), _ptr(yc), _ptr(g), xc.numel() // C, C, DTYPE_CODE[x.dtype],
+              _ptr(out), _stream(xc))
+    return out

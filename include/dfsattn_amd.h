@@ -239,6 +239,29 @@ int dfs_head_norm_rope(const void* x, int64_t x_sb, int64_t x_sl, int64_t x_sh,
                        const float* sin_table, int64_t rope_rows,
                        dfs_stream_t stream);
 
+/*
+ * DiT block elementwise steps around the attention (the Wan transformer
+ * block of diffusers that the reference's Wan driver loads,
+ * wan21_t2v_inference.py:102-103; not part of the reference's own code).
+ * x, out: [rows][channels] contiguous, bf16 or f16; fp32 vectors of
+ * `channels` entries, each optional (NULL skips its step):
+ *   out = (LayerNorm(x, eps) * weight + bias) * (1 + scale) + shift,
+ * the LayerNorm over the channels in fp32 (biased variance), every product
+ * and sum rounded in fp32 in that order, the result rounded to dtype.
+ * channels: a multiple of 8, at most 8192.
+ */
+int dfs_adaln_modulate(const void* x, int64_t rows, int64_t channels,
+                       int dtype, const float* weight, const float* bias,
+                       const float* scale, const float* shift, float eps,
+                       void* out, dfs_stream_t stream);
+
+/* out = x + y * gate (gate fp32 [channels], broadcast over rows), computed
+ * in fp32 (product rounded, then the sum) and rounded to dtype; x, y, out
+ * [rows][channels] contiguous bf16 or f16 (out may alias x). */
+int dfs_gated_residual(const void* x, const void* y, const float* gate,
+                       int64_t rows, int64_t channels, int dtype, void* out,
+                       dfs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
