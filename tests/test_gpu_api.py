@@ -249,3 +249,35 @@ def test_overflow_check_reruns_on_bf16_operands(dev):
     p, inv = orc.full_permutation(perm, q.shape[2])
     ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
     assert _rel(out.cpu(), ref) < 6e-3  # bf16 operands and output
+
+
+@pytest.mark.parametrize("grid,heads,d,dtype,sparsity", [
+    ((1, 10, 10), 1, 64, torch.bfloat16, 0.3),     # 100 tokens: one partial block
+    ((1, 3, 43), 2, 128, torch.float16, 0.3),      # 129 tokens: a last block of one token
+    ((2, 16, 24), 2, 128, torch.bfloat16, 1.0),    # every block kept
+    ((2, 16, 24), 3, 64, torch.bfloat16, 0.01),    # k = max(1, int(s * Kb)) = 1
+])
+def test_wan_edge_shapes_match_oracle(dev, grid, heads, d, dtype, sparsity):
+    """dfs_attention at boundary sizes and sparsities against the oracle's
+    whole call (mask from the oracle's fp32 scores, attention on the GPU's
+    own mask)."""
+    from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+
+    cfg = DfsConfig("edge", grid, heads, d, dtype, seed=11)
+    q, k, v = synth_qkv(cfg)
+    perm = hilbert3d_perm(*grid)
+    print(f"edge case grid={grid} heads={heads} d={d} {dtype} s={sparsity}", flush=True)
+    out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=24, skip_steps=12, cache_interval=12,
+                        layer_idx=7, sparsity=sparsity, sparsity_dcrt=0.0, tile_size=16, video_perm=perm)
+    assert out.shape == q.shape and out.dtype == dtype
+    mask = DFS_Attention._cached_metadata[(7, "native", 128, 16, 16)]["block_mask"].cpu()
+    _, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, sparsity, 16)
+    assert (mask == ref_mask).float().mean() > 0.95
+    kb = mask.shape[-1]
+    assert bool((mask.sum(-1) == max(1, int(sparsity * kb))).all())
+    p, inv = orc.full_permutation(perm, q.shape[2])
+    ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
+    assert _rel(out.cpu(), ref) < 4e-3
+    assert float((out.cpu().float() - ref).abs().max()) < 2e-2
