@@ -36,6 +36,7 @@ class DFS_Attention(DfsCore, nn.Module):
     density_records: Dict[int, Dict[int, float]] = {}
     sparsity_records: Dict[int, Dict[int, Dict[str, Any]]] = {}
     timing_recorder = AttentionTimingRecorder()
+    _entry_fields = ("block_mask", "frontier_mask")  # attention_hyvideo.py:1178-1183
 
     def __init__(self, step_idx: int, layer_idx: int, sparse_ratio: float = 0.5, cache_flag: bool = True,
                  video_len: int = 0, video_perm: Optional[torch.Tensor] = None, block_size: int = 128,

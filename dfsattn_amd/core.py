@@ -77,6 +77,9 @@ class DfsCore:
     # device-to-host read per call) and the call is redone on bf16 operands
     # when any is found; False (default) keeps the call free of host syncs.
     check_overflow: bool = False
+    # The fields a cache entry holds in the reference (attention_wan.py:466-470);
+    # get_cache_info counts these per entry, as the reference does (:664-670).
+    _entry_fields: Tuple[str, ...] = ("block_mask", "block_indices", "flex_block_mask")
 
     def _prepare(self, q, k, v, perm, layout, pool: bool) -> "ops.Prepared":
         od = operand_dtype_for(q.dtype, self.operand_dtype)
@@ -152,7 +155,7 @@ class DfsCore:
         row_ptr = row_ptr_for(policy, prep.heads, prep.q_perm.device)
         col_idx, scores, _ = ops.block_score_topk(prep, policy, row_ptr, want_scores=want_scores)
         entry = MaskEntry(row_ptr=row_ptr, col_idx=col_idx, policy=policy, heads=prep.heads,
-                          block_mask=None, block_indices=None, flex_block_mask=None)
+                          **{field: None for field in self._entry_fields})
         if want_scores:
             dict.__setitem__(entry, "block_scores", scores)
         return entry
@@ -296,7 +299,8 @@ class DfsCore:
         return {
             "num_cached_steps": len(cls._cached_metadata),
             "cached_steps": list(cls._cached_metadata.keys()),
-            "total_cached_layers": sum(len(v) for v in cls._cached_metadata.values()),
+            "total_cached_layers": sum(sum(1 for f in cls._entry_fields if f in v)
+                                       for v in cls._cached_metadata.values()),
         }
 
 

@@ -84,3 +84,28 @@ def test_density_records_csv(tmp_path, capsys):
     assert "Mean execution-tile density: 0.5833" in printed
     assert "Mean per-step execution-tile density: 0.6875" in printed
     DFS_Attention.execution_tile_records.clear()
+
+
+@pytest.mark.parametrize("module, per_entry", [("attention_wan", 3), ("attention_hyvideo", 2)])
+def test_cache_info_counts_reference_fields(module, per_entry):
+    """get_cache_info counts the fields the reference stores per entry
+    (attention_wan.py:466-470, 664-670; attention_hyvideo.py:1178-1183),
+    not this build's extra CSR fields."""
+    import importlib
+
+    from dfsattn_amd.core import MaskEntry
+
+    cls = importlib.import_module(f"dfsattn_amd.{module}").DFS_Attention
+    saved = dict(cls._cached_metadata)
+    try:
+        cls._cached_metadata.clear()
+        for layer in range(2):
+            cls._cached_metadata[(layer, "native")] = MaskEntry(
+                row_ptr=None, col_idx=None, policy=None, heads=1, **{f: None for f in cls._entry_fields})
+        info = cls.get_cache_info()
+        assert info["num_cached_steps"] == 2
+        assert info["cached_steps"] == [(0, "native"), (1, "native")]
+        assert info["total_cached_layers"] == 2 * per_entry
+    finally:
+        cls._cached_metadata.clear()
+        cls._cached_metadata.update(saved)
