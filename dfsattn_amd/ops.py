@@ -28,10 +28,26 @@ def _stream(t: torch.Tensor):
 
 
 def _require_device(*tensors: Optional[torch.Tensor]) -> None:
+    """Every given tensor lives on one and the same ROCm device."""
+    first = None
     for t in tensors:
-        if t is not None and t.device.type != "cuda":
+        if t is None:
+            continue
+        if t.device.type != "cuda":
             raise RuntimeError(
                 "DFS kernels run on a ROCm GPU only; got a tensor on " + str(t.device))
+        if first is None:
+            first = t.device
+        elif t.device != first:
+            raise RuntimeError(f"DFS kernel operands must share one device, got {first} and {t.device}")
+
+
+def _require_int32(**tensors: Optional[torch.Tensor]) -> None:
+    """Index operands (permutations, CSR offsets and columns) are contiguous int32."""
+    for name, t in tensors.items():
+        if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous int32 tensor, got {t.dtype}"
+                             f"{'' if t.is_contiguous() else ' (non-contiguous)'}")
 
 
 def _heads_rows(x: torch.Tensor) -> Tuple[int, int, int]:
@@ -59,6 +75,7 @@ def device_perm(perm: torch.Tensor, device: torch.device) -> torch.Tensor:
 def permute_gather(src: torch.Tensor, perm: torch.Tensor, rows: Optional[int] = None) -> torch.Tensor:
     """out[..., i, :] = src[..., perm[i], :] (rows >= len(perm) zero)."""
     _require_device(src, perm)
+    _require_int32(perm=perm)
     heads, length, dim = _heads_rows(src)
     src = src.contiguous()
     n = perm.numel()
@@ -73,6 +90,9 @@ def permute_scatter(src: torch.Tensor, perm: torch.Tensor, out: Optional[torch.T
                     rows: Optional[int] = None) -> torch.Tensor:
     """out[..., perm[i], :] = src[..., i, :] for i < len(perm)."""
     _require_device(src, perm, out)
+    _require_int32(perm=perm)
+    if out is not None and (out.dtype != src.dtype or not out.is_contiguous() or out.shape[-1] != src.shape[-1]):
+        raise ValueError("out must be a contiguous tensor of src's dtype and row width")
     heads, length, dim = _heads_rows(src)
     src = src.contiguous()
     n = perm.numel()
@@ -113,6 +133,7 @@ def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.T
     inputs to f16; bf16 keeps their bits. ``check_overflow`` allocates a flag
     set when a finite input exceeds the f16 range."""
     _require_device(q, k, v, perm)
+    _require_int32(perm=perm)
     heads, length, dim = _heads_rows(q)
     if q.dtype not in (torch.bfloat16, torch.float16):
         raise RuntimeError("DFS native attention only supports fp16 and bf16 inputs")
@@ -162,6 +183,10 @@ def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
     119k)."""
     if prep.q_hi is None:
         raise ValueError("prepare_qkv was called without pooling")
+    _require_device(prep.q_hi, row_ptr)
+    _require_int32(row_ptr=row_ptr)
+    if row_ptr.numel() != prep.heads * policy.q_blocks + 1:
+        raise ValueError(f"row_ptr has {row_ptr.numel()} entries for {prep.heads} x {policy.q_blocks} rows")
     dev = prep.q_perm.device
     nnz = policy.nnz(prep.heads)
     col_idx = torch.empty(nnz, dtype=torch.int32, device=dev)
@@ -179,6 +204,7 @@ def topk_from_scores(scores: torch.Tensor, policy: TopkPolicy, row_ptr: torch.Te
     """Top-k of given fp32 block scores [H, scored_rows, Kb] under ``policy``;
     returns (col_idx, mask or None)."""
     _require_device(scores, row_ptr)
+    _require_int32(row_ptr=row_ptr)
     if scores.dtype != torch.float32 or scores.dim() != 3:
         raise ValueError("scores must be fp32 [H, rows, Kb]")
     heads = scores.shape[0]
@@ -199,7 +225,10 @@ def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale:
     """Block-sparse attention over the CSR mask. Returns out [1, H, L, D] —
     original token order when ``out_perm`` is given, execution order otherwise —
     and the fp32 log-sum-exp [H, L] (execution order) when ``want_lse``."""
-    _require_device(row_ptr, col_idx, out_perm, out)
+    _require_device(prep.q_perm, row_ptr, col_idx, out_perm, out)
+    _require_int32(row_ptr=row_ptr, col_idx=col_idx, out_perm=out_perm)
+    if row_ptr.numel() != prep.heads * prep.layout.q_blocks + 1:
+        raise ValueError(f"row_ptr has {row_ptr.numel()} entries for {prep.heads} x {prep.layout.q_blocks} rows")
     L = prep.layout.seq_len
     out_dtype = out_dtype or prep.dtype
     if out is None:
@@ -230,13 +259,16 @@ def mask_to_csr(mask: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     nnz = int(row_ptr[-1].item())
     col_idx = torch.empty(max(nnz, 1), dtype=torch.int32, device=m.device)
     _lib.call("dfs_mask_to_csr", _ptr(m), rows, m.shape[-1], _ptr(row_ptr), _ptr(col_idx), _stream(m))
-    return row_ptr, col_idx[:nnz] if nnz else col_idx
+    return row_ptr, col_idx[:nnz]  # storage of at least one element: never a NULL pointer
 
 
 def csr_to_mask(row_ptr: torch.Tensor, col_idx: torch.Tensor, heads: int, q_blocks: int,
                 k_blocks: int) -> torch.Tensor:
     """CSR -> bool mask [H, Qb, Kb] on the device."""
     _require_device(row_ptr, col_idx)
+    _require_int32(row_ptr=row_ptr, col_idx=col_idx)
+    if row_ptr.numel() != heads * q_blocks + 1:
+        raise ValueError(f"row_ptr has {row_ptr.numel()} entries for {heads} x {q_blocks} rows")
     mask = torch.empty((heads, q_blocks, k_blocks), dtype=torch.uint8, device=row_ptr.device)
     _lib.call("dfs_csr_to_mask", _ptr(row_ptr), _ptr(col_idx), heads * q_blocks, k_blocks, _ptr(mask),
               _stream(row_ptr))

@@ -369,3 +369,37 @@ def test_bsa_fwd_rising_and_negative_logits(dev, monkeypatch, schedule):
     assert torch.isfinite(out).all()
     assert float((out - ref).abs().max()) <= 2e-2 and mean_rel(out, ref) <= 1e-3, \
         (float((out - ref).abs().max()), mean_rel(out, ref))
+
+
+def test_wrappers_reject_bad_index_operands(dev):
+    """Index operands must be contiguous int32 on the operands' device, and
+    CSR offsets must cover every (head, query block) row: checked on the host
+    before any launch."""
+    length, heads = 300, 2
+    q = torch.randn(1, heads, length, 64).bfloat16().to(dev)
+    layout = ScoringLayout(length, length, 16)
+    ident = torch.arange(length, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        ops.prepare_qkv(q, q, q, ident.long(), layout)
+    with pytest.raises(ValueError):
+        ops.permute_gather(q, ident.long())
+    prep = ops.prepare_qkv(q, q, q, ident, layout)
+    pol = wan_policy(layout, 0.5)
+    row_ptr = torch.from_numpy(pol.row_ptr(heads)).to(dev)
+    col_idx, _, _ = ops.block_score_topk(prep, pol, row_ptr)
+    with pytest.raises(ValueError):
+        ops.bsa_fwd(prep, row_ptr.long(), col_idx)
+    with pytest.raises(ValueError):
+        ops.bsa_fwd(prep, row_ptr[:-1].contiguous(), col_idx)
+    with pytest.raises(ValueError):
+        ops.bsa_fwd(prep, row_ptr, col_idx, out_perm=ident.long())
+    with pytest.raises(ValueError):
+        ops.block_score_topk(prep, pol, row_ptr[1:].contiguous())
+    with pytest.raises(ValueError):
+        ops.csr_to_mask(row_ptr, col_idx.long(), heads, pol.q_blocks, pol.k_blocks)
+    with pytest.raises(RuntimeError):
+        ops.bsa_fwd(prep, row_ptr.cpu(), col_idx)
+    # the valid call still runs after the rejections
+    out = ops.bsa_fwd(prep, row_ptr, col_idx, out_perm=ident)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all())
