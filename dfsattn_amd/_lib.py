@@ -25,8 +25,9 @@ SIGNATURES = {
     "dfs_permute_scatter": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
     "dfs_prepare_qkv": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _i64, _i32,
                         _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    "dfs_block_score_topk_workspace_size": [_i64, _i64, _i64, _i64],
     "dfs_block_score_topk": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                             _i64, _i64, _i64, _p, _p, _p, _p, _p],
+                             _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p],
     "dfs_topk_from_scores": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p],
     "dfs_bsa_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _p, _i32, _p, _p, _p],
     "dfs_mask_row_counts": [_p, _i64, _i64, _p, _p],
@@ -39,8 +40,8 @@ SIGNATURES = {
     "dfs_adaln_modulate": [_p, _i64, _i64, _i32, _p, _p, _p, _p, _f32, _p, _p],
     "dfs_gated_residual": [_p, _p, _p, _i64, _i64, _i32, _p, _p],
 }
-_RESTYPES = {"dfs_last_error": ctypes.c_char_p}
-ABI_VERSION = 1
+_RESTYPES = {"dfs_last_error": ctypes.c_char_p, "dfs_block_score_topk_workspace_size": ctypes.c_int64}
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib = None

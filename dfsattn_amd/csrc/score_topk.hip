@@ -127,6 +127,9 @@ struct ScoreParams {
   int32_t* col_idx;
   float* scores_out;
   uint8_t* mask_out;
+  float* tile_sums;  // one-pass: [H][tile_rows][tile_cols] unnormalised tile-block sums
+  int64_t tile_rows;
+  int tile_cols;
   Policy pol;
   int q_tiles, k_tiles;
   float scale_log2;
@@ -292,7 +295,7 @@ __global__ void __launch_bounds__(256) score_topk_kernel(ScoreParams p) {
 // GB (global block sums): the block sums go straight to scores_out (which
 // the caller provides) instead of LDS, so a workgroup needs only its key
 // chunks and the top-k histograms in LDS and four workgroups fit on a CU.
-template <int D, int TPB, bool GB>
+template <int D, int TPB, bool GB, bool ONE_PASS = false>
 __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) {
   constexpr int CPR = D / 8;             // 16-byte chunks per pooled row
   constexpr int QBW = 32 / TPB;          // query blocks per wave
@@ -356,6 +359,95 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     };
 
     issue(0);
+    if constexpr (ONE_PASS) {
+      // One pass: exp2(s - m) against a reference m shared by the two lane
+      // halves of a query tile (the first chunk's maximum; moved only when a
+      // chunk's sum exceeds 2^64, as below), summed per (query tile, key
+      // block) into the workspace row of the tile while the normaliser z
+      // accumulates; the rows are scaled by 1/Z and summed into blocks at the
+      // end. Half the MFMA work of the two-pass form.
+      const int qrow = blockIdx.x * G * TPB + w * 32 + l32;  // this lane's tile row in the workspace
+      float* urow = p.tile_sums + (static_cast<int64_t>(h) * p.tile_rows + qrow) * p.tile_cols;
+      constexpr int BPC = ROWS / TPB;  // key blocks per chunk
+      float m = -INFINITY, z = 0.f;
+      for (int c = 0; c < nchunks; ++c) {
+        wait_vmcnt_0();
+        block_barrier();
+        issue(c + 1);
+        if (!wave_scores) continue;
+        const f32x16 acc = chunk_scores(c & 1);
+        const int lim = (c + 1) * ROWS <= p.k_tiles ? ROWS : p.k_tiles - c * ROWS;  // valid key tiles
+        auto joint_max = [&]() {
+          float cm = -INFINITY;
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (acc_row(r, hl) < lim) cm = fmaxf(cm, acc[r] * p.scale_log2);
+          return fmaxf(cm, __shfl_xor(cm, 32));
+        };
+        float pr[16];
+        auto exps = [&]() {
+          float sum = 0.f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            pr[r] = acc_row(r, hl) < lim ? exp2_fast(fmaf(acc[r], p.scale_log2, -m)) : 0.f;
+            sum += pr[r];
+          }
+          return sum;
+        };
+        if (!(m > -INFINITY)) m = joint_max();  // the first chunk with valid keys
+        float sum = exps();
+        int ovf = !(sum <= 0x1p64f);
+        ovf |= __shfl_xor(ovf, 32);
+        if (__any(ovf)) {
+          if (ovf) {  // a logit far above the reference: move it to this chunk's maximum
+            const float mn = fmaxf(m, joint_max());
+            const float f = exp2_fast(m - mn);
+            z *= f;
+            __threadfence_block();  // this lane's earlier row stores are visible to its loads
+            for (int j = hl; j < c * BPC; j += 2) urow[j] *= f;
+            m = mn;
+          }
+          sum = exps();
+        }
+        z += sum;
+        if constexpr (TPB == 8) {
+          float u[4];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            u[b] = (pr[4 * b] + pr[4 * b + 1]) + (pr[4 * b + 2] + pr[4 * b + 3]);
+            u[b] += __shfl_xor(u[b], 32);
+          }
+          if (hl == 0) *reinterpret_cast<float4*>(urow + c * 4) = make_float4(u[0], u[1], u[2], u[3]);
+        } else {
+#pragma unroll
+          for (int gg = 0; gg < 4; ++gg)
+            urow[c * 8 + 2 * gg + hl] = (pr[4 * gg] + pr[4 * gg + 1]) + (pr[4 * gg + 2] + pr[4 * gg + 3]);
+        }
+      }
+      wait_vmcnt_0();  // the trailing (empty) copies have retired
+      if (wave_scores) {
+        const float Z = z + __shfl_xor(z, 32);  // same reference in both halves
+        const float invZ = Z > 0.f ? 1.0f / Z : 0.f;
+        __threadfence_block();  // the rows written above are visible to the wave's loads
+        // Block sums: lane (tile l32, half hl) scales 4 columns of its row,
+        // then the TPB tiles of a query block are summed by shuffles.
+        for (int kb0 = hl * 4; kb0 < nchunks * BPC; kb0 += 8) {
+          const float4 t = *reinterpret_cast<const float4*>(urow + kb0);
+          float v[4] = {t.x * invZ, t.y * invZ, t.z * invZ, t.w * invZ};
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int off = 1; off < TPB; off <<= 1) v[j] += __shfl_xor(v[j], off);
+          const int g = w * QBW + l32 / TPB;
+          if ((l32 & (TPB - 1)) == 0 && (!GB || qb0 + g < pol.scored_rows)) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (kb0 + j < pol.Kb) bsum[g * pol.Kb + kb0 + j] = v[j];
+          }
+        }
+      }
+      __syncthreads();  // the block sums are visible to the workgroup
+    } else {
     // Pass 1: normaliser z of every query tile (one per lane half) against a
     // reference m in the log2 domain: m is the maximum of the tile's first
     // chunk; later chunks add exp2(s - m) without a maximum, and only a
@@ -458,6 +550,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     }
     wait_vmcnt_0();  // the trailing (empty) copies have retired
     __syncthreads();  // with GB: the block sums in global memory are visible to the workgroup
+    }
     if (!GB && p.scores_out) {
       for (int i = tid; i < G * pol.Kb; i += 256) {
         const int g = i / pol.Kb, col = i - g * pol.Kb;
@@ -534,12 +627,22 @@ int check_policy(const char* name, int64_t heads, int64_t q_blocks, int64_t k_bl
 
 extern "C" {
 
+int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t tile_size, int64_t q_blocks,
+                                            int64_t k_blocks) {
+  if (heads <= 0 || q_blocks <= 0 || k_blocks <= 0 || (tile_size != 16 && tile_size != 32)) return -1;
+  const int64_t tpb = dfs::kBlock / tile_size, Gw = 4 * (32 / tpb);
+  const int64_t rows = (q_blocks + Gw - 1) / Gw * Gw * tpb;        // tile rows of every workgroup
+  const int64_t cols = (k_blocks * tpb + 31) / 32 * (32 / tpb);  // key blocks of every 32-tile chunk
+  return heads * rows * cols * static_cast<int64_t>(sizeof(float));
+}
+
 int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
                          const uint16_t* k_pool_hi, const uint16_t* k_pool_lo, int64_t heads,
                          int64_t head_dim, int64_t tile_size, int64_t q_blocks, int64_t k_blocks,
                          int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
                          int64_t dense_row, const int32_t* row_ptr, int32_t* col_idx,
-                         float* scores_out, uint8_t* mask_out, dfs_stream_t stream) {
+                         float* scores_out, uint8_t* mask_out, void* workspace, int64_t workspace_bytes,
+                         dfs_stream_t stream) {
   using namespace dfs;
   const char* name = "dfs_block_score_topk";
   DFS_REQUIRE(q_pool_hi && q_pool_lo && k_pool_hi && k_pool_lo && row_ptr && col_idx,
@@ -579,6 +682,27 @@ int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
   p.k_tiles = static_cast<int>(k_blocks * tpb);
   p.scale_log2 = static_cast<float>(1.4426950408889634 / sqrt(static_cast<double>(head_dim)));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (workspace) {
+    DFS_REQUIRE(global_sums, "%s: the one-pass form (workspace given) needs scores_out", name);
+    const int64_t need = dfs_block_score_topk_workspace_size(heads, tile_size, q_blocks, k_blocks);
+    DFS_REQUIRE(workspace_bytes >= need, "%s: workspace of %lld bytes, %lld needed", name,
+                (long long)workspace_bytes, (long long)need);
+    DFS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "%s: workspace must be 16-byte aligned",
+                name);
+    p.tile_sums = static_cast<float*>(workspace);
+    p.tile_rows = (q_blocks + Gw - 1) / Gw * Gw * tpb;
+    p.tile_cols = static_cast<int>((k_blocks * tpb + 31) / 32 * (32 / tpb));
+    dim3 grid(static_cast<unsigned>((q_blocks + Gw - 1) / Gw), static_cast<unsigned>(heads));
+    if (head_dim == 128 && tpb == 8)
+      score_topk_wide_kernel<128, 8, true, true><<<grid, 256, smem_gb, s>>>(p);
+    else if (head_dim == 128)
+      score_topk_wide_kernel<128, 4, true, true><<<grid, 256, smem_gb, s>>>(p);
+    else if (tpb == 8)
+      score_topk_wide_kernel<64, 8, true, true><<<grid, 256, smem_gb, s>>>(p);
+    else
+      score_topk_wide_kernel<64, 4, true, true><<<grid, 256, smem_gb, s>>>(p);
+    return check_launch(name);
+  }
   if (global_sums) {
     dim3 grid(static_cast<unsigned>((q_blocks + Gw - 1) / Gw), static_cast<unsigned>(heads));
     if (head_dim == 128 && tpb == 8)

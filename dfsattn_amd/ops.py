@@ -174,13 +174,22 @@ def _policy_args(policy: TopkPolicy):
             policy.dense_col, policy.dense_row)
 
 
+def score_workspace_bytes(heads: int, tile: int, q_blocks: int, k_blocks: int) -> int:
+    """Bytes of the one-pass scoring workspace (per-tile partial block sums)."""
+    n = int(_lib.lib().dfs_block_score_topk_workspace_size(heads, tile, q_blocks, k_blocks))
+    if n < 0:
+        raise ValueError(f"no scoring workspace for heads={heads} tile={tile} blocks={q_blocks}x{k_blocks}")
+    return n
+
+
 def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
-                     want_scores: bool = False, want_mask: bool = False):
+                     want_scores: bool = False, want_mask: bool = False, one_pass: bool = True):
     """Scores + top-k: returns (col_idx int32 [nnz], scores fp32 [H,Vb,Kb] or
     None, mask uint8 [H,Qb,Kb] or None). The score matrix is always passed
     to the kernel, which then keeps its block sums there rather than in LDS
-    (more workgroups per CU: 1.5 -> 1.36 ms at 75.6k tokens, 4.0 -> 2.1 ms at
-    119k)."""
+    (more workgroups per CU). With ``one_pass`` a workspace of per-tile
+    partial sums lets the kernel score every tile pair once instead of twice
+    (normaliser pass, then block-sum pass)."""
     if prep.q_hi is None:
         raise ValueError("prepare_qkv was called without pooling")
     _require_device(prep.q_hi, row_ptr)
@@ -193,9 +202,13 @@ def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
     scores = torch.empty((prep.heads, policy.scored_rows, policy.k_blocks), dtype=torch.float32, device=dev)
     mask = (torch.empty((prep.heads, policy.q_blocks, policy.k_blocks), dtype=torch.uint8, device=dev)
             if want_mask else None)
+    ws, ws_bytes = None, 0
+    if one_pass:
+        ws_bytes = score_workspace_bytes(prep.heads, prep.layout.tile, policy.q_blocks, policy.k_blocks)
+        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
     _lib.call("dfs_block_score_topk", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi), _ptr(prep.k_lo),
               prep.heads, prep.head_dim, prep.layout.tile, *_policy_args(policy), _ptr(row_ptr),
-              _ptr(col_idx), _ptr(scores), _ptr(mask), _stream(prep.q_perm))
+              _ptr(col_idx), _ptr(scores), _ptr(mask), _ptr(ws), ws_bytes, _stream(prep.q_perm))
     return col_idx, (scores if want_scores else None), mask
 
 

@@ -39,7 +39,7 @@ enum { DFS_DTYPE_BF16 = 0, DFS_DTYPE_F16 = 1, DFS_DTYPE_F32 = 2 };
 /* Last error message of the calling thread ("" if none). */
 const char* dfs_last_error(void);
 
-/* ABI version; bumped whenever a signature below changes. */
+/* ABI version; bumped whenever a signature below changes (2: scoring workspace). */
 int dfs_abi_version(void);
 
 /*
@@ -118,6 +118,11 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v,
  *                of in LDS, which lets more workgroups share a CU (faster;
  *                rows from dense_row on are then scored too).
  *   mask_out     optional uint8 [H][Qb][Kb] block mask.
+ *   workspace    optional device buffer of workspace_bytes >= the size from
+ *                dfs_block_score_topk_workspace_size (16-byte aligned; needs
+ *                scores_out). With it the kernel scores every tile pair once,
+ *                keeping unnormalised per-tile block sums there, instead of
+ *                twice (a normaliser pass, then a block-sum pass).
  * Ties are broken by (score descending, column ascending).
  * Replaces _compute_tile_score + _compute_block_mask
  * (attention_wan.py:157-261; attention_hyvideo.py:310-501).
@@ -130,7 +135,17 @@ int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
                          int64_t dense_col, int64_t dense_row,
                          const int32_t* row_ptr, int32_t* col_idx,
                          float* scores_out, uint8_t* mask_out,
+                         void* workspace, int64_t workspace_bytes,
                          dfs_stream_t stream);
+
+/*
+ * Bytes of the optional dfs_block_score_topk workspace for these sizes
+ * (-1 for invalid sizes). Host function; no reference counterpart (the
+ * reference materialises the whole [H, Qt, Kt] tile-score tensor instead,
+ * attention_wan.py:207-209).
+ */
+int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t tile_size,
+                                            int64_t q_blocks, int64_t k_blocks);
 
 /*
  * Top-k from given fp32 block scores [H][scored_rows][Kb] with the policy

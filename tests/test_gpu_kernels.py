@@ -192,7 +192,9 @@ def test_block_score_topk_matches_oracle(dev, d, tile, video, text):
 @pytest.mark.parametrize("video,text", [(4 * 16 * 16 * 4, 0), (2000, 100)])
 def test_block_score_topk_lds_sums_path_selects_the_same(dev, video, text):
     """dfs_block_score_topk without a score matrix keeps its block sums in
-    LDS; its selection equals the global-sums path's."""
+    LDS; its selection equals the two-pass global-sums path's (the same
+    arithmetic), and the one-pass path's scores agree with both to fp32
+    rounding."""
     import ctypes
     from dfsattn_amd import _lib
     from dfsattn_amd.ops import _policy_args
@@ -206,13 +208,45 @@ def test_block_score_topk_lds_sums_path_selects_the_same(dev, video, text):
     pol = wan_policy(layout, 0.3) if text == 0 else hunyuan_policy(layout, 0.3)
     row_ptr = torch.from_numpy(pol.row_ptr(heads)).to(dev)
     prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout)
-    col_global, _, _ = ops.block_score_topk(prep, pol, row_ptr)
+    col_global, scores2, _ = ops.block_score_topk(prep, pol, row_ptr, want_scores=True, one_pass=False)
     col_lds = torch.empty_like(col_global)
     p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     _lib.call("dfs_block_score_topk", p(prep.q_hi), p(prep.q_lo), p(prep.k_hi), p(prep.k_lo), heads, 128, 16,
-              *_policy_args(pol), p(row_ptr), p(col_lds), None, None,
+              *_policy_args(pol), p(row_ptr), p(col_lds), None, None, None, 0,
               ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
     assert torch.equal(col_lds.cpu(), col_global.cpu())
+    _, scores1, _ = ops.block_score_topk(prep, pol, row_ptr, want_scores=True, one_pass=True)
+    torch.testing.assert_close(scores1.cpu(), scores2.cpu(), rtol=2e-5, atol=1e-7)
+
+
+def test_block_score_topk_workspace_checks(dev):
+    """The one-pass form needs a large enough, aligned workspace and a score matrix."""
+    import ctypes
+    from dfsattn_amd import _lib
+    from dfsattn_amd.ops import _policy_args, score_workspace_bytes
+    heads, length = 2, 1000
+    q = torch.randn(1, heads, length, 64).bfloat16().to(dev)
+    layout = ScoringLayout(length, length, 16)
+    pol = wan_policy(layout, 0.3)
+    row_ptr = torch.from_numpy(pol.row_ptr(heads)).to(dev)
+    prep = ops.prepare_qkv(q, q, q, torch.arange(length, dtype=torch.int32, device=dev), layout)
+    need = score_workspace_bytes(heads, 16, pol.q_blocks, pol.k_blocks)
+    # rows of 16 query blocks per workgroup x 8 tiles, key blocks padded to 32-tile chunks
+    assert need == heads * 16 * 8 * 8 * 4
+    ws = torch.empty(need // 4 + 4, dtype=torch.float32, device=dev)
+    col = torch.empty(pol.nnz(heads), dtype=torch.int32, device=dev)
+    scores = torch.empty((heads, pol.scored_rows, pol.k_blocks), dtype=torch.float32, device=dev)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    args = (p(prep.q_hi), p(prep.q_lo), p(prep.k_hi), p(prep.k_lo), heads, 64, 16, *_policy_args(pol), p(row_ptr),
+            p(col))
+    for sc, w, nbytes in ((p(scores), p(ws), need - 4), (None, p(ws), need),
+                          (p(scores), ctypes.c_void_p(ws.data_ptr() + 4), need)):
+        with pytest.raises(_lib.DfsKernelError):
+            _lib.call("dfs_block_score_topk", *args, sc, None, w, nbytes, stream)
+    _lib.call("dfs_block_score_topk", *args, p(scores), None, p(ws), need, stream)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(scores).all())
 
 
 @pytest.mark.parametrize("direction", ["rising", "falling"])

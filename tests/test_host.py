@@ -17,7 +17,7 @@ HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))
 
 def test_library_exports_every_declared_symbol():
     text = open(HEADER).read()
-    declared = set(re.findall(r"^\s*(?:int|const char\*)\s+(dfs_\w+)\s*\(", text, flags=re.M))
+    declared = set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(dfs_\w+)\s*\(", text, flags=re.M))
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
     lib = _lib.lib()
     for name in declared:
