@@ -164,30 +164,31 @@ class DfsCore:
         return ops.bsa_fwd(prep, entry["row_ptr"], entry["col_idx"], scale=None, out_dtype=prep.dtype,
                            out_perm=perm)
 
-    def _execute_segments(self, q, k, v, entry: MaskEntry, perm: torch.Tensor, valid: int) -> torch.Tensor:
+    def _execute_segments(self, q, k, v, prep: ops.Prepared, entry: MaskEntry, perm: torch.Tensor,
+                          valid: int) -> torch.Tensor:
         """cu_seqlens [0, valid, L] (attention_hyvideo.py:1054-1082): the
         external kernel runs the valid tokens and the padding tokens as two
         sequences, each with the same block mask indexed from its own first
         token (the mask is repeated per sequence). Valid tokens come first in
         execution order (the permutation moves video tokens only), so the
-        segments are the execution rows [0, valid) and [valid, L)."""
+        valid segment is execution rows [0, valid): it runs on the call's own
+        operands and CSR mask, restricted to its leading rows and keys. The
+        padding segment [valid, L) gets its own operands and the mask's
+        leading blocks, without a host round-trip, and its rows are copied
+        into the output."""
         seq_len = q.shape[2]
-        mask = entry["block_mask"]
-        outs = []
-        for start, end in ((0, valid), (valid, seq_len)):
-            n = end - start
-            if n <= 0:
-                continue
-            nb = math.ceil(n / self.block_size)
-            sub = mask[:, :nb, :nb].contiguous()
-            row_ptr, col_idx = ops.mask_to_csr(sub)
-            seg_perm = perm[start:end] - start if start else perm[:end]
-            q_s, k_s, v_s = (x[:, :, start:end] for x in (q, k, v))
-            lay = ScoringLayout(n, n, 16, self.block_size)
-            prep = self._prepare(q_s, k_s, v_s, seg_perm.contiguous(), lay, pool=False)
-            outs.append(ops.bsa_fwd(prep, row_ptr, col_idx, scale=None, out_dtype=prep.dtype,
-                                    out_perm=seg_perm.contiguous()))
-        return torch.cat(outs, dim=2)
+        out = ops.bsa_fwd(prep, entry["row_ptr"], entry["col_idx"], scale=None, out_dtype=prep.dtype,
+                          out_perm=perm, valid_len=valid)
+        n = seq_len - valid
+        nb = math.ceil(n / self.block_size)
+        row_ptr, col_idx = ops.mask_to_csr(entry["block_mask"][:, :nb, :nb].contiguous(), exact=False)
+        seg_perm = (perm[valid:] - valid).contiguous()
+        lay = ScoringLayout(n, n, 16, self.block_size)
+        q_s, k_s, v_s = (x[:, :, valid:] for x in (q, k, v))
+        pad_prep = self._prepare(q_s, k_s, v_s, seg_perm, lay, pool=False)
+        out[:, :, valid:] = ops.bsa_fwd(pad_prep, row_ptr, col_idx, scale=None, out_dtype=prep.dtype,
+                                        out_perm=seg_perm)
+        return out
 
     @staticmethod
     def _tile_counts(entry: MaskEntry) -> np.ndarray:
@@ -239,7 +240,7 @@ class DfsCore:
             self._record_density(entry, seq_len)
         t_att = rec.start(device)
         if valid < seq_len:
-            out = self._execute_segments(q, k, v, entry, perm, valid)
+            out = self._execute_segments(q, k, v, prep, entry, perm, valid)
         else:
             out = self._execute(prep, entry, perm)
         rec.stop(t_att, phase="attention_execution", step_idx=self.step_idx, layer_idx=self.layer_idx, device=device)

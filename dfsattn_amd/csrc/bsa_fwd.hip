@@ -43,7 +43,10 @@ namespace dfs {
 namespace {
 
 struct BsaParams {
-  int H, L, R, Qb, Kb;
+  // L: valid length (query rows computed, keys attended); R: operand rows per
+  // head; Lo: out / lse rows per head; Qb = Kb = ceil(L / 128); csr_qb: CSR
+  // rows per head (the mask may have been selected over a longer sequence).
+  int H, L, R, Qb, Kb, Lo, csr_qb;
   int sched;   // workgroup order: 0 head-major across XCDs, 1 XCD-contiguous
   int rotate;  // rotated key-block sweep (split schedule)
   int pair_order;  // partner-first column order (split schedule, default)
@@ -366,7 +369,7 @@ __device__ __forceinline__ void store_out(const BsaParams& p, void* __restrict__
   const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
   if (qrow >= p.L) return;
   const int orow = out_perm ? out_perm[qrow] : qrow;
-  const int64_t obase = (static_cast<int64_t>(h) * p.L + orow) * D;
+  const int64_t obase = (static_cast<int64_t>(h) * p.Lo + orow) * D;
 #pragma unroll
   for (int dc = 0; dc < DCH; ++dc)
 #pragma unroll
@@ -387,7 +390,7 @@ __device__ __forceinline__ void store_out(const BsaParams& p, void* __restrict__
       }
     }
   if (lse && hl == 0)
-    lse[static_cast<int64_t>(h) * p.L + qrow] = ltot > 0.f ? (m + log2f(ltot)) * 0.69314718055994531f : -INFINITY;
+    lse[static_cast<int64_t>(h) * p.Lo + qrow] = ltot > 0.f ? (m + log2f(ltot)) * 0.69314718055994531f : -INFINITY;
 }
 
 #define BSA_KERNEL_ARGS                                                                                \
@@ -411,7 +414,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
   int h, qb;
   if (!wg_coords(p, h, qb)) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int64_t row = static_cast<int64_t>(h) * p.Qb + qb;
+  const int64_t row = static_cast<int64_t>(h) * p.csr_qb + qb;
   const int beg = row_ptr[row];
   const int end = beg + min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
   const int qrow = qb * 128 + w * 32 + l32;
@@ -457,7 +460,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
       }
       const int qp = qb ^ 1;
       if (qp < p.Qb) {
-        const int64_t prow = static_cast<int64_t>(h) * p.Qb + qp;
+        const int64_t prow = static_cast<int64_t>(h) * p.csr_qb + qp;
         const int pbeg = row_ptr[prow];
         const int pn = min(max(row_ptr[prow + 1] - pbeg, 0), p.Kb);
         for (int i = tid; i < pn; i += 256) {
@@ -720,7 +723,7 @@ __global__ void __launch_bounds__(512, 1) bsa_fwd_pp_kernel(BSA_KERNEL_ARGS) {
   for (int r = 0; r < 2; ++r) {
     const int qr = grp * 2 + r;
     if (qr < p.Qb) {
-      const int64_t row = static_cast<int64_t>(h) * p.Qb + qr;
+      const int64_t row = static_cast<int64_t>(h) * p.csr_qb + qr;
       const int beg = row_ptr[row];
       const int cnt = min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
       for (int i = tid; i < cnt; i += 512) {
@@ -903,7 +906,7 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
                            const int32_t* row_ptr, const int32_t* col_idx, int64_t heads,
                            int64_t seq_len, int64_t head_dim, int dtype, int pv_dtype, float scale,
                            void* out, int out_dtype, const int32_t* out_perm, float* lse,
-                           dfs_stream_t stream) {
+                           int64_t valid_len, dfs_stream_t stream) {
   using namespace dfs;
   const char* name = "dfs_bsa_fwd";
   DFS_REQUIRE(q_perm && k_perm && v_t && row_ptr && col_idx && out, "%s: NULL operand", name);
@@ -923,14 +926,20 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   // LDS: 64 KB of tiles (split schedule) plus the row's column list.
   DFS_REQUIRE(qb <= 8192, "%s: %lld key blocks exceed the LDS column list", name, (long long)qb);
   DFS_REQUIRE(scale > 0.f && isfinite(scale), "%s: scale must be positive and finite", name);
+  if (valid_len == 0) valid_len = seq_len;
+  DFS_REQUIRE(valid_len > 0 && valid_len <= seq_len, "%s: valid_len=%lld outside [1, %lld]", name,
+              (long long)valid_len, (long long)seq_len);
+  const int64_t vb = (valid_len + kBlock - 1) / kBlock;
   BsaArgs a{static_cast<const uint16_t*>(q_perm), static_cast<const uint16_t*>(k_perm),
             static_cast<const uint16_t*>(v_t), row_ptr, col_idx, out, out_perm, lse};
   BsaParams p{};
   p.H = static_cast<int>(heads);
-  p.L = static_cast<int>(seq_len);
+  p.L = static_cast<int>(valid_len);
   p.R = static_cast<int>(qb * kBlock);
-  p.Qb = static_cast<int>(qb);
-  p.Kb = static_cast<int>(qb);
+  p.Qb = static_cast<int>(vb);
+  p.Kb = static_cast<int>(vb);
+  p.Lo = static_cast<int>(seq_len);
+  p.csr_qb = static_cast<int>(qb);
   p.scale_log2 = scale * 1.4426950408889634f;
   p.out_kind = out_dtype;
   const char* order = getenv("DFSATTN_AMD_BSA_SCHED");
@@ -938,7 +947,8 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   const char* po = getenv("DFSATTN_AMD_BSA_ORDER");
   // DFSATTN_AMD_BSA_ORDER: "pair" (default, partner-first) or "rotate"
   // (each row's own ascending list from a workgroup-dependent start).
-  p.pair_order = (po && strcmp(po, "rotate") == 0) ? 0 : 1;
+  // A valid length below seq_len needs the bitmap orders, which drop columns >= Kb.
+  p.pair_order = (po && strcmp(po, "rotate") == 0 && valid_len == seq_len) ? 0 : 1;
   const char* rot = getenv("DFSATTN_AMD_BSA_ROTATE");
   p.rotate = (rot && rot[0] == '0') ? 0 : 1;
   const char* kern = getenv("DFSATTN_AMD_BSA_KERNEL");

@@ -234,15 +234,20 @@ def topk_from_scores(scores: torch.Tensor, policy: TopkPolicy, row_ptr: torch.Te
 
 def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale: Optional[float] = None,
             out_dtype: Optional[torch.dtype] = None, out_perm: Optional[torch.Tensor] = None,
-            want_lse: bool = False, out: Optional[torch.Tensor] = None):
+            want_lse: bool = False, out: Optional[torch.Tensor] = None, valid_len: Optional[int] = None):
     """Block-sparse attention over the CSR mask. Returns out [1, H, L, D] —
     original token order when ``out_perm`` is given, execution order otherwise —
-    and the fp32 log-sum-exp [H, L] (execution order) when ``want_lse``."""
+    and the fp32 log-sum-exp [H, L] (execution order) when ``want_lse``.
+    ``valid_len`` < L restricts the call to the first valid_len execution
+    rows and keys (the mask's leading blocks; rows from valid_len on are not
+    written)."""
     _require_device(prep.q_perm, row_ptr, col_idx, out_perm, out)
     _require_int32(row_ptr=row_ptr, col_idx=col_idx, out_perm=out_perm)
     if row_ptr.numel() != prep.heads * prep.layout.q_blocks + 1:
         raise ValueError(f"row_ptr has {row_ptr.numel()} entries for {prep.heads} x {prep.layout.q_blocks} rows")
     L = prep.layout.seq_len
+    if valid_len is not None and not 0 < valid_len <= L:
+        raise ValueError(f"valid_len {valid_len} outside [1, {L}]")
     out_dtype = out_dtype or prep.dtype
     if out is None:
         out = torch.empty((1, prep.heads, L, prep.head_dim), dtype=out_dtype, device=prep.q_perm.device)
@@ -253,13 +258,15 @@ def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale:
     _lib.call("dfs_bsa_fwd", _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(row_ptr),
               _ptr(col_idx), prep.heads, L, prep.head_dim, DTYPE_CODE[prep.operand_dtype],
               DTYPE_CODE[prep.operand_dtype], scale, _ptr(out), DTYPE_CODE[out_dtype], _ptr(out_perm),
-              _ptr(lse), _stream(prep.q_perm))
+              _ptr(lse), int(valid_len or 0), _stream(prep.q_perm))
     return (out, lse) if want_lse else out
 
 
-def mask_to_csr(mask: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+def mask_to_csr(mask: torch.Tensor, exact: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
     """bool/uint8 [H, Qb, Kb] mask -> (row_ptr int32 [H*Qb+1], col_idx int32).
-    Reads the total count back to the host once to size col_idx."""
+    With ``exact`` the total count is read back to the host once to size
+    col_idx; otherwise col_idx has room for every block (no host sync) and
+    only its first row_ptr[-1] entries are meaningful."""
     _require_device(mask)
     m = mask.contiguous()
     if m.dtype == torch.bool:
@@ -269,7 +276,7 @@ def mask_to_csr(mask: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     _lib.call("dfs_mask_row_counts", _ptr(m), rows, m.shape[-1], _ptr(counts), _stream(m))
     row_ptr = torch.zeros(rows + 1, dtype=torch.int32, device=m.device)
     torch.cumsum(counts, 0, out=row_ptr[1:])
-    nnz = int(row_ptr[-1].item())
+    nnz = int(row_ptr[-1].item()) if exact else m.numel()
     col_idx = torch.empty(max(nnz, 1), dtype=torch.int32, device=m.device)
     _lib.call("dfs_mask_to_csr", _ptr(m), rows, m.shape[-1], _ptr(row_ptr), _ptr(col_idx), _stream(m))
     return row_ptr, col_idx[:nnz]  # storage of at least one element: never a NULL pointer

@@ -39,7 +39,7 @@ enum { DFS_DTYPE_BF16 = 0, DFS_DTYPE_F16 = 1, DFS_DTYPE_F32 = 2 };
 /* Last error message of the calling thread ("" if none). */
 const char* dfs_last_error(void);
 
-/* ABI version; bumped whenever a signature below changes (2: scoring workspace). */
+/* ABI version; bumped whenever a signature below changes (2: scoring workspace, attention valid_len). */
 int dfs_abi_version(void);
 
 /*
@@ -174,7 +174,15 @@ int dfs_topk_from_scores(const float* scores, int64_t heads,
  *                        written to out[h][out_perm[i]] (fused unpermute).
  *   lse                  optional fp32 [H][L] natural-log sum-exp (execution
  *                        order).
- * Keys >= L in the last block are masked out; rows with no kept block give 0.
+ *   valid_len            0 (or L): the whole sequence. 0 < valid_len < L: only
+ *                        execution rows and keys below valid_len take part
+ *                        (columns >= ceil(valid_len/128) of the CSR rows are
+ *                        skipped; rows from valid_len on are not written): the
+ *                        first of the two sequences of cu_seqlens [0, valid, L]
+ *                        (attention_hyvideo.py:1054-1082), run on the whole
+ *                        call's operands and mask. CSR columns must ascend.
+ * Keys >= valid_len in the last block are masked out; rows with no kept
+ * block give 0.
  * Replaces block_sparse_attn_func (attention_wan.py:379-386;
  * attention_hyvideo.py:1075-1082) and, with out_perm, the final inverse
  * gather (attention_wan.py:390).
@@ -183,7 +191,8 @@ int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v_t,
                 const int32_t* row_ptr, const int32_t* col_idx,
                 int64_t heads, int64_t seq_len, int64_t head_dim, int dtype,
                 int pv_dtype, float scale, void* out, int out_dtype,
-                const int32_t* out_perm, float* lse, dfs_stream_t stream);
+                const int32_t* out_perm, float* lse, int64_t valid_len,
+                dfs_stream_t stream);
 
 /* uint8/bool block mask [H][Qb][Kb] -> per-row counts int32 [H*Qb].
  * Part of the bool-mask interface of block_sparse_attn_func

@@ -437,3 +437,32 @@ def test_wrappers_reject_bad_index_operands(dev):
     out = ops.bsa_fwd(prep, row_ptr, col_idx, out_perm=ident)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out.float()).all())
+
+
+@pytest.mark.parametrize("schedule", ("pp", "split"))
+@pytest.mark.parametrize("length,valid", [(1300, 1100), (1300, 1152), (1000, 130), (1000, 1)])
+def test_bsa_fwd_valid_len_is_the_leading_sequence(dev, monkeypatch, schedule, length, valid):
+    """valid_len restricts a call to the first rows and keys: the result
+    equals masked attention of the leading sequence under the mask's leading
+    blocks (columns past them, kept in the CSR rows, are skipped), and rows
+    from valid_len on are left as they were."""
+    _set_schedule(monkeypatch, schedule)
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+    heads, d = 2, 128
+    cfg = DfsConfig("t", (1, 1, length), heads, d, torch.bfloat16, seed=21)
+    q, k, v = synth_qkv(cfg)
+    nb, vb = math.ceil(length / 128), math.ceil(valid / 128)
+    g = torch.Generator().manual_seed(22)
+    mask = torch.rand((heads, nb, nb), generator=g) < 0.4
+    mask[:, torch.arange(nb), torch.arange(nb)] = True
+    layout = ScoringLayout(length, length, 16)
+    ident = torch.arange(length, dtype=torch.int32)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident.to(dev), layout, pool=False)
+    row_ptr, col_idx = ops.mask_to_csr(mask.to(dev))
+    out = torch.full((1, heads, length, d), 7.0, dtype=torch.float32, device=dev)
+    ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=torch.float32, out=out, valid_len=valid)
+    out = out.cpu()
+    ref = orc.masked_attention(q[:, :, :valid], k[:, :, :valid], v[:, :, :valid], mask[:, :vb, :vb])
+    got = out[:, :, :valid]
+    assert float((got - ref).abs().max()) <= 2e-2 and mean_rel(got, ref) <= 1e-3
+    assert bool((out[:, :, valid:] == 7.0).all())

@@ -43,7 +43,10 @@ def test_abi_rejects_bad_arguments_without_launching():
         _lib.call("dfs_topk_from_scores", fake, 2, 8, 8, 8, 8, 9, 8, 8, fake, fake, None, None)
     with pytest.raises(_lib.DfsKernelError, match="f16 inputs"):
         _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 0, 0.1, fake, 2,
-                  None, None, None)
+                  None, None, 0, None)
+    with pytest.raises(_lib.DfsKernelError, match="valid_len"):
+        _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 1, 0.1, fake, 2,
+                  None, None, 1001, None)
     with pytest.raises(_lib.DfsKernelError, match="row_bytes"):
         _lib.call("dfs_permute_gather", fake, fake, fake, 1, 10, 10, 10, 3, None)
     with pytest.raises(_lib.DfsKernelError, match="positive"):
