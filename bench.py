@@ -169,11 +169,19 @@ def run_cfg2(args):
     log("generating cfg2 inputs on the GPU")
     q, k, v = synth_qkv(cfg, device=dev)
     perm = hilbert3d_perm(*cfg.grid)
+    seg = {}
+    if args.text_valid is not None:
+        # text padded to 256 tokens with text_valid of them valid: cu_seqlens [0, valid, L]
+        # (replace_hyvideo.py:221-228), the valid and padding tokens as two sequences
+        if not 0 <= args.text_valid < cfg.text_len:
+            raise SystemExit(f"--text-valid must lie in [0, {cfg.text_len})")
+        cu = torch.tensor([0, cfg.video_len + args.text_valid, cfg.seq_len], dtype=torch.int32)
+        seg = dict(cu_seqlens_q=cu, cu_seqlens_kv=cu)
 
     def step():
         return dfs_attention(q, k, v, step_idx=12, skip_steps=12, cache_interval=12, layer_idx=0,
                              sparsity=cfg.sparsity, sparsity_dcrt=0.0, tile_size=cfg.tile, block_size=cfg.block,
-                             video_len=cfg.video_len, video_perm=perm, cache_flag=True)
+                             video_len=cfg.video_len, video_perm=perm, cache_flag=True, **seg)
 
     for i in range(args.warmup):
         step()
@@ -192,12 +200,15 @@ def run_cfg2(args):
     DFS_Attention.clear_cache()
     _dfs_attention_instances.clear()
     log(f"cfg2: {ms:.3f} ms/call, {flops / ms / 1e9:.1f} effective TFLOP/s")
+    pad = ("" if args.text_valid is None else
+           f", text padding: {args.text_valid} valid text tokens, cu_seqlens [0, valid, L] (FLOP counted on the "
+           "whole-sequence mask)")
     return {"metric": "DFS attn ms/call @119,056 tok (118,800 video + 256 text),24h,d128 bf16",
             "value": round(ms, 3), "unit": "ms/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
             "dtype": "bf16", "data": "synthetic (smoothed-field Q/K, iid V, iid text; seeded)",
             "config": {"workload": "cfg2 HunyuanVideo joint attention: 33x45x80 video + 256 text tokens, 24 heads, "
-                                   "d128, tile 16, block 128, hilbert3d, sparsity 0.3, fresh mask per call",
+                                   "d128, tile 16, block 128, hilbert3d, sparsity 0.3, fresh mask per call" + pad,
                        "global_batch": 1, "seq_len": cfg.seq_len, "parallelism": "none (1 GPU)"},
             "effective_tflops": round(flops / ms / 1e9, 1), "kept_flop": flops,
             "frac_of_bf16_peak": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
@@ -421,6 +432,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", choices=("cfg1", "cfg2", "cfg3", "cfg4"), default="cfg1")
+    ap.add_argument("--text-valid", type=int, default=None,
+                    help="cfg2: valid text tokens of the 256 (the rest padding, cu_seqlens [0, valid, L])")
     ap.add_argument("--dit-phase", choices=("both", "dfs", "dense"), default="both",
                     help="cfg4: time the DFS step, the dense step or both")
     args = ap.parse_args()
