@@ -127,9 +127,8 @@ struct ScoreParams {
   int32_t* col_idx;
   float* scores_out;
   uint8_t* mask_out;
-  float* tile_sums;  // one-pass: [H][tile_rows][tile_cols] unnormalised tile-block sums
-  int64_t tile_rows;
-  int tile_cols;
+  float* tile_sums;  // one pass: [H][workgroup][tile_cols][tiles of the workgroup] unnormalised block sums
+  int tile_cols;     // key blocks of all 32-tile chunks (Kb rounded up to a chunk)
   Policy pol;
   int q_tiles, k_tiles;
   float scale_log2;
@@ -366,8 +365,13 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       // block) into the workspace row of the tile while the normaliser z
       // accumulates; the rows are scaled by 1/Z and summed into blocks at the
       // end. Half the MFMA work of the two-pass form.
-      const int qrow = blockIdx.x * G * TPB + w * 32 + l32;  // this lane's tile row in the workspace
-      float* urow = p.tile_sums + (static_cast<int64_t>(h) * p.tile_rows + qrow) * p.tile_cols;
+      // Workspace of this workgroup: [tile_cols][G * TPB] (key block major), so
+      // the 32 tiles of a wave write and read each key block's sums as one
+      // contiguous 128-byte line. U(kb) is this lane's tile's sum for key block kb.
+      constexpr int WG_TILES = G * TPB;
+      float* const ubase = p.tile_sums +
+                           (static_cast<int64_t>(h) * gridDim.x + blockIdx.x) * p.tile_cols * WG_TILES + w * 32 + l32;
+      auto U = [&](int kb) -> float& { return ubase[static_cast<int64_t>(kb) * WG_TILES]; };
       constexpr int BPC = ROWS / TPB;  // key blocks per chunk
       float m = -INFINITY, z = 0.f;
       for (int c = 0; c < nchunks; ++c) {
@@ -404,7 +408,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
             const float f = exp2_fast(m - mn);
             z *= f;
             __threadfence_block();  // this lane's earlier row stores are visible to its loads
-            for (int j = hl; j < c * BPC; j += 2) urow[j] *= f;
+            for (int j = hl; j < c * BPC; j += 2) U(j) *= f;
             m = mn;
           }
           sum = exps();
@@ -417,11 +421,12 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
             u[b] = (pr[4 * b] + pr[4 * b + 1]) + (pr[4 * b + 2] + pr[4 * b + 3]);
             u[b] += __shfl_xor(u[b], 32);
           }
-          if (hl == 0) *reinterpret_cast<float4*>(urow + c * 4) = make_float4(u[0], u[1], u[2], u[3]);
+          U(c * 4 + 2 * hl) = hl ? u[2] : u[0];  // the two halves store two key blocks each
+          U(c * 4 + 2 * hl + 1) = hl ? u[3] : u[1];
         } else {
 #pragma unroll
           for (int gg = 0; gg < 4; ++gg)
-            urow[c * 8 + 2 * gg + hl] = (pr[4 * gg] + pr[4 * gg + 1]) + (pr[4 * gg + 2] + pr[4 * gg + 3]);
+            U(c * 8 + 2 * gg + hl) = (pr[4 * gg] + pr[4 * gg + 1]) + (pr[4 * gg + 2] + pr[4 * gg + 3]);
         }
       }
       wait_vmcnt_0();  // the trailing (empty) copies have retired
@@ -432,8 +437,9 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
         // Block sums: lane (tile l32, half hl) scales 4 columns of its row,
         // then the TPB tiles of a query block are summed by shuffles.
         for (int kb0 = hl * 4; kb0 < nchunks * BPC; kb0 += 8) {
-          const float4 t = *reinterpret_cast<const float4*>(urow + kb0);
-          float v[4] = {t.x * invZ, t.y * invZ, t.z * invZ, t.w * invZ};
+          float v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = U(kb0 + j) * invZ;
 #pragma unroll
           for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -690,7 +696,6 @@ int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
     DFS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "%s: workspace must be 16-byte aligned",
                 name);
     p.tile_sums = static_cast<float*>(workspace);
-    p.tile_rows = (q_blocks + Gw - 1) / Gw * Gw * tpb;
     p.tile_cols = static_cast<int>((k_blocks * tpb + 31) / 32 * (32 / tpb));
     dim3 grid(static_cast<unsigned>((q_blocks + Gw - 1) / Gw), static_cast<unsigned>(heads));
     if (head_dim == 128 && tpb == 8)
