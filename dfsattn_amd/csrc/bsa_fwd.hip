@@ -20,7 +20,8 @@
 //    reference maximum comes from its first block and later blocks skip the
 //    maximum (a block is redone only if its P overflows f16); the LDS operand
 //    reads run four MFMAs ahead, and the QK phase runs at raised wave
-//    priority.
+//    priority. A row visits its key blocks in order of distance from its own
+//    block, so neighbouring query blocks fetch shared key blocks together.
 //  * ping-pong (DFSATTN_AMD_BSA_KERNEL=pp, f16 operands): one eight-wave
 //    workgroup per CU for two adjacent query blocks, the two four-wave groups
 //    alternating MFMA and softmax phases half a cycle apart (described at the
@@ -49,7 +50,8 @@ struct BsaParams {
   int H, L, R, Qb, Kb, Lo, csr_qb;
   int sched;   // workgroup order: 0 head-major across XCDs, 1 XCD-contiguous
   int rotate;  // rotated key-block sweep (split schedule)
-  int pair_order;  // partner-first column order (split schedule, default)
+  int pair_order;  // bitmap-built column order (split schedule, default): by distance from the diagonal
+  int partner;     // ... with the columns shared with the partner row (qb ^ 1) first
   float scale_log2;
   int out_kind;  // 0 bf16, 1 f16, 2 f32
 };
@@ -445,27 +447,38 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
     // Q fragments forced complete here so no wait for them lands in the loop.
     int n = end - beg;
     if (p.pair_order) {
-      // Partner-first order: the columns this row shares with its partner row
-      // (query block qb ^ 1, run by the neighbouring workgroup of the same
-      // XCD at about the same time) first, both ascending, then the rest. The
-      // partner fetches the shared key blocks in the same order, so one of
-      // the two reads of each mostly hits L2.
-      const int W = (p.Kb + 31) >> 5;
+      // Diagonal-distance order: the row's columns by distance |c - qb| from
+      // its own block (c = qb first, then qb - 1, qb + 1, qb - 2, ...). The
+      // workgroups resident on an XCD at one time run neighbouring Hilbert
+      // query blocks, whose kept columns cluster around their diagonals, so
+      // they fetch the same key blocks at about the same time (2% fewer L2
+      // misses than ascending partner-first order, 0.4-1.2% faster). Columns
+      // live in a bitmap at bit 2|c - qb| + (c > qb), compacted in bit order.
+      // With partner set, the columns shared with the partner row (query
+      // block qb ^ 1) come first, each group in distance order.
+      const int W = (2 * p.Kb + 31) >> 5;
+      auto bpos = [&](int c) { return 2 * (c >= qb ? c - qb : qb - c) + (c > qb ? 1 : 0); };
       uint32_t* bm = reinterpret_cast<uint32_t*>(cols + p.Kb);  // [own W][partner W]
       for (int i = tid; i < 2 * W; i += 256) bm[i] = 0u;
       block_barrier();
       for (int i = tid; i < n; i += 256) {
         const int c = col_idx[beg + i];
-        if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) atomicOr(&bm[c >> 5], 1u << (c & 31));
+        if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) {
+          const int b = bpos(c);
+          atomicOr(&bm[b >> 5], 1u << (b & 31));
+        }
       }
       const int qp = qb ^ 1;
-      if (qp < p.Qb) {
+      if (p.partner && qp < p.Qb) {
         const int64_t prow = static_cast<int64_t>(h) * p.csr_qb + qp;
         const int pbeg = row_ptr[prow];
         const int pn = min(max(row_ptr[prow + 1] - pbeg, 0), p.Kb);
         for (int i = tid; i < pn; i += 256) {
           const int c = col_idx[pbeg + i];
-          if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) atomicOr(&bm[W + (c >> 5)], 1u << (c & 31));
+          if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) {
+            const int b = bpos(c);
+            atomicOr(&bm[W + (b >> 5)], 1u << (b & 31));
+          }
         }
       }
       block_barrier();
@@ -492,12 +505,14 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
           const uint32_t own = bm[w0 + j], par = bm[W + w0 + j];
           uint32_t x = own & par;
           while (x) {
-            cols[ps++] = (w0 + j) * 32 + __ffs(x) - 1;
+            const int b = (w0 + j) * 32 + __ffs(x) - 1;
+            cols[ps++] = (b & 1) ? qb + (b >> 1) : qb - (b >> 1);
             x &= x - 1;
           }
           x = own & ~par;
           while (x) {
-            cols[po++] = (w0 + j) * 32 + __ffs(x) - 1;
+            const int b = (w0 + j) * 32 + __ffs(x) - 1;
+            cols[po++] = (b & 1) ? qb + (b >> 1) : qb - (b >> 1);
             x &= x - 1;
           }
         }
@@ -884,7 +899,7 @@ void launch_typed(const BsaArgs& a, const BsaParams& p, BsaSchedule sched, hipSt
   const int S = (p.Qb + 7) / 8;
   dim3 grid(static_cast<unsigned>(p.sched == 0 ? 8 * S * p.H : p.H * p.Qb));
   const size_t smem = static_cast<size_t>(p.Kb) * sizeof(int32_t) +
-                      (p.pair_order ? static_cast<size_t>(2 * ((p.Kb + 31) / 32)) * sizeof(uint32_t) : 0);
+                      (p.pair_order ? static_cast<size_t>(2 * ((2 * p.Kb + 31) / 32)) * sizeof(uint32_t) : 0);
   bsa_fwd_split_kernel<D, QK_F16, PV_F16><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
                                                                  a.out_perm, a.lse, p);
 }
@@ -945,10 +960,12 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   const char* order = getenv("DFSATTN_AMD_BSA_SCHED");
   p.sched = (order && order[0] == '1') ? 1 : 0;
   const char* po = getenv("DFSATTN_AMD_BSA_ORDER");
-  // DFSATTN_AMD_BSA_ORDER: "pair" (default, partner-first) or "rotate"
-  // (each row's own ascending list from a workgroup-dependent start).
+  // DFSATTN_AMD_BSA_ORDER: unset (default, diagonal-distance order), "pair"
+  // (partner-shared columns first, then the rest, each by distance) or
+  // "rotate" (each row's own ascending list from a workgroup-dependent start).
   // A valid length below seq_len needs the bitmap orders, which drop columns >= Kb.
   p.pair_order = (po && strcmp(po, "rotate") == 0 && valid_len == seq_len) ? 0 : 1;
+  p.partner = (po && strcmp(po, "pair") == 0) ? 1 : 0;
   const char* rot = getenv("DFSATTN_AMD_BSA_ROTATE");
   p.rotate = (rot && rot[0] == '0') ? 0 : 1;
   const char* kern = getenv("DFSATTN_AMD_BSA_KERNEL");

@@ -285,7 +285,7 @@ def _run_bsa(dev, q, k, v, mask_bool, pv, out_dtype, perm=None):
     return out.cpu()
 
 
-SCHEDULES = ("pp", "split", "split+rotate")
+SCHEDULES = ("pp", "split", "split+pair", "split+rotate")
 
 
 def _set_schedule(monkeypatch, schedule):
