@@ -4,12 +4,15 @@
 // dfsattn/attention_hyvideo.py:310-501): with pooled tile means q_i, k_j,
 //   P[i, j]      = softmax_j( q_i . k_j * D^-1/2 )   over ALL key tiles j
 //   score[a, b]  = sum_{i in query block a} sum_{j in key block b} P[i, j]
-// followed by a top-k over each row a. One workgroup owns 32 query tiles of one
-// head; its four waves stream the pooled key tiles in 32-tile chunks through
-// bf16 MFMAs on a hi/lo split (q.k ~= qh.kh + qh.kl + ql.kh, relative error
-// ~2^-16), so the scores track the fp32 computation closely. Pass 1 builds the
-// per-tile softmax max / normaliser, pass 2 accumulates block sums in LDS, and
-// the same workgroup then selects the top-k of every row it owns, one wave per
+// followed by a top-k over each row a. In the default (wide) kernel each of a
+// workgroup's four waves owns 32 query tiles of one head; the workgroup streams
+// the head's pooled key tiles in 32-tile chunks through LDS into bf16 MFMAs on
+// a hi/lo split (q.k ~= qh.kh + qh.kl + ql.kh, relative error ~2^-16), so the
+// scores track the fp32 computation closely. With a caller workspace the
+// scores are made in one pass (per-tile block sums kept in the workspace while
+// the softmax normaliser accumulates, scaled at the end); without one, pass 1
+// builds the normaliser and pass 2 recomputes the scores into block sums. The
+// same workgroup then selects the top-k of every row it owns, one wave per
 // row, emitting CSR column indices for the attention kernel.
 #include <math.h>
 
