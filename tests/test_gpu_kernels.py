@@ -250,10 +250,12 @@ def test_block_score_topk_workspace_checks(dev):
 
 
 @pytest.mark.parametrize("direction", ["rising", "falling"])
-def test_block_scores_with_far_apart_logits(dev, direction):
+@pytest.mark.parametrize("tile,one_pass", [(16, True), (32, True), (16, False), (32, False)])
+def test_block_scores_with_far_apart_logits(dev, direction, tile, one_pass):
     """Key tiles whose logits rise (or fall) by ~130 log2 units across the
     row: the scoring pass's reference (the first chunk's maximum) has to
-    move for rising logits and stays for falling ones; both match the fp32
+    move for rising logits (in the one-pass form, rescaling the block sums
+    already stored) and stays for falling ones; every form matches the fp32
     softmax of the oracle."""
     length, d = 2048, 128
     ramp = torch.linspace(0.0, 8.0, length)
@@ -262,13 +264,13 @@ def test_block_scores_with_far_apart_logits(dev, direction):
     q = torch.ones(1, 1, length, d).bfloat16()
     k = (ramp[None, None, :, None] * torch.ones(1, 1, length, d)).bfloat16()
     v = torch.zeros_like(q)
-    layout = ScoringLayout(length, length, 16)
+    layout = ScoringLayout(length, length, tile)
     pol = wan_policy(layout, 0.3)
     row_ptr = torch.from_numpy(pol.row_ptr(1)).to(dev)
     ident = torch.arange(length, dtype=torch.int32)
     prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident.to(dev), layout)
-    _, scores, _ = ops.block_score_topk(prep, pol, row_ptr, want_scores=True)
-    ref = orc.block_scores(q.float(), k.float(), 16, 128, None)
+    _, scores, _ = ops.block_score_topk(prep, pol, row_ptr, want_scores=True, one_pass=one_pass)
+    ref = orc.block_scores(q.float(), k.float(), tile, 128, None)
     got = scores.cpu()
     assert bool(torch.isfinite(got).all())
     assert torch.allclose(got, ref, rtol=2e-3, atol=2e-5), float((got - ref).abs().max())
