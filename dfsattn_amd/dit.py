@@ -166,8 +166,18 @@ class DiTBlock(nn.Module):
 
     # On the GPU the layer norms with their modulation and the gated residuals
     # run as one fused pass each (dfs_adaln_modulate, dfs_gated_residual)
-    # instead of torch's chain of dtype copies and broadcast ops.
+    # instead of torch's chain of dtype copies and broadcast ops, and the FFN's
+    # GELU runs in the first GEMM's epilogue (hipBLASLt, through torch's
+    # _addmm_activation: 8.2 -> 7.5 ms per call at 75,600 x 5,120 x 13,824; the
+    # activation is applied before the bf16 rounding instead of after it).
     fused_elementwise: bool = True
+
+    def _ffn_fused(self, h: torch.Tensor) -> torch.Tensor:
+        lin1, act, lin2 = self.ffn
+        if lin1.bias is None or not hasattr(torch, "_addmm_activation"):
+            return self.ffn(h)
+        a = torch._addmm_activation(lin1.bias, h.reshape(-1, h.shape[-1]), lin1.weight.t(), use_gelu=True)
+        return lin2(a).reshape(*h.shape[:-1], -1)
 
     def forward(self, x: torch.Tensor, context: torch.Tensor, temb: torch.Tensor,
                 rotary_emb: torch.Tensor) -> torch.Tensor:
@@ -180,7 +190,7 @@ class DiTBlock(nn.Module):
             h = ops.adaln_modulate(x, self.norm2.eps, weight=self.norm2.weight.float(), bias=self.norm2.bias.float())
             x = x + self.attn2(h, context)
             h = ops.adaln_modulate(x, self.norm3.eps, scale=c_scale, shift=c_shift)
-            return ops.gated_residual(x, self.ffn(h), c_gate)
+            return ops.gated_residual(x, self._ffn_fused(h), c_gate)
         h = (self.norm1(x.float()) * (1 + scale_msa) + shift_msa).type_as(x)
         x = (x.float() + self.attn1(h, None, None, rotary_emb) * gate_msa).type_as(x)
         h = self.norm2(x.float()).type_as(x)
