@@ -58,7 +58,8 @@ def test_permute_gather_scatter_bit_exact(dev, dtype, d, length, n):
     assert torch.count_nonzero(back[:, :, untouched]) == 0
 
 
-@pytest.mark.parametrize("case", ["wan_tail", "wan_even", "hunyuan_text", "hunyuan_no_text", "d64_tile32"])
+@pytest.mark.parametrize("case", ["wan_tail", "wan_even", "hunyuan_text", "hunyuan_no_text", "d64_tile32",
+                                  "tile8", "d64_tile64"])
 def test_prepare_qkv_matches_oracle(dev, case):
     heads, d, tile, dtype, pv = 2, 128, 16, torch.bfloat16, torch.float16
     if case == "wan_tail":
@@ -69,6 +70,10 @@ def test_prepare_qkv_matches_oracle(dev, case):
         length, video = 1000 + 60, 1000
     elif case == "hunyuan_no_text":
         length, video = 1000, 1000
+    elif case == "tile8":  # tile sizes the scorer does not take are still prepared
+        length, video, tile = 1000 + 40, 1000, 8
+    elif case == "d64_tile64":
+        length, video, d, tile = 900, 900, 64, 64
     else:
         length, video, d, tile, pv = 777, 777, 64, 32, torch.bfloat16
     torch.manual_seed(7)
