@@ -81,3 +81,52 @@ def test_full_size_call(dev, cfg_id):
     assert _rel(g, r) < 4e-3  # includes the bf16 rounding of the output
     DFS_Attention.clear_cache()
     _dfs_attention_instances.clear()
+
+
+def test_full_size_hunyuan_text_padding(dev):
+    """configs[2] with 30 of the 256 text tokens valid (cu_seqlens [0, valid,
+    L], replace_hyvideo.py:221-228): the mask is selected over the whole
+    sequence; sampled query blocks of the valid segment match fp32 masked
+    attention over the leading valid tokens under the mask's leading blocks,
+    and the padding segment matches its own masked attention (the mask's
+    first blocks, indexed from the segment's first token)."""
+    import math
+
+    from dfsattn_amd import ops
+    from dfsattn_amd.attention_hyvideo import DFS_Attention, _dfs_attention_instances, dfs_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[2]
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()
+    q, k, v = synth_qkv(cfg, device=dev)
+    perm = hilbert3d_perm(*cfg.grid)
+    L, H = cfg.seq_len, cfg.heads
+    valid = cfg.video_len + 30
+    cu = torch.tensor([0, valid, L], dtype=torch.int32)
+    out = dfs_attention(q, k, v, step_idx=12, skip_steps=12, cache_interval=12, layer_idx=0,
+                        sparsity=cfg.sparsity, sparsity_dcrt=0.0, tile_size=cfg.tile, video_len=cfg.video_len,
+                        video_perm=perm, cu_seqlens_q=cu, cu_seqlens_kv=cu)
+    torch.cuda.synchronize()
+    entry = next(iter(DFS_Attention._cached_metadata.values()))
+    mask = entry["block_mask"].cpu()
+    full, _ = orc.full_permutation(perm, L)
+    heads = [0, H - 1]
+    sub = [orc.apply_permutation(t[:, heads].float().cpu(), full) for t in (q, k, v)]
+    got_out = out[:, heads].cpu()[:, :, full].float()  # execution order
+    # valid segment: execution rows [0, valid)
+    vb = math.ceil(valid / 128)
+    qbs = [0, vb // 2, vb - 2, vb - 1]
+    ref = orc.masked_attention(*(t[:, :, :valid] for t in sub), mask[heads][:, :vb, :vb], 128, q_blocks=qbs)
+    rows = torch.cat([torch.arange(b * 128, min((b + 1) * 128, valid)) for b in qbs])
+    g, r = got_out[:, :, rows], ref[:, :, rows]
+    assert float((g - r).abs().max()) < 2e-2 and _rel(g, r) < 4e-3
+    # padding segment: execution rows [valid, L), its own block indices
+    n = L - valid
+    nb = math.ceil(n / 128)
+    ref_p = orc.masked_attention(*(t[:, :, valid:] for t in sub), mask[heads][:, :nb, :nb], 128)
+    g, r = got_out[:, :, valid:], ref_p
+    assert float((g - r).abs().max()) < 2e-2 and _rel(g, r) < 4e-3
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()
