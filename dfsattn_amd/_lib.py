@@ -29,7 +29,8 @@ SIGNATURES = {
     "dfs_block_score_topk": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p],
     "dfs_topk_from_scores": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p],
-    "dfs_bsa_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _p, _i32, _p, _p, _i64, _p],
+    "dfs_prepare_fixup": [_p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p],
+    "dfs_bsa_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _p, _i32, _p, _p, _p, _p, _i64, _p, _p],
     "dfs_mask_row_counts": [_p, _i64, _i64, _p, _p],
     "dfs_mask_to_csr": [_p, _i64, _i64, _p, _p, _p],
     "dfs_csr_to_mask": [_p, _p, _i64, _i64, _p, _p],
@@ -41,7 +42,7 @@ SIGNATURES = {
     "dfs_gated_residual": [_p, _p, _p, _i64, _i64, _i32, _p, _p],
 }
 _RESTYPES = {"dfs_last_error": ctypes.c_char_p, "dfs_block_score_topk_workspace_size": ctypes.c_int64}
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib = None

@@ -8,7 +8,6 @@ cached mask is reused without any host round-trip.
 """
 from __future__ import annotations
 
-import math
 from typing import Any, Dict, Optional, Tuple
 
 import numpy as np
@@ -16,7 +15,6 @@ import torch
 
 from . import ops
 from .layout import ScoringLayout, TopkPolicy
-from .utils.logger import logger
 
 SUPPORTED_EXECUTION = "native"
 
@@ -60,7 +58,8 @@ class MaskEntry(dict):
 
 def operand_dtype_for(dtype: torch.dtype, requested: Optional[torch.dtype]) -> torch.dtype:
     """Attention operand precision: f16 by default (Q * scale * log2(e), K, V
-    and P rounded to 11 bits keep the output within 1e-3 mean-rel of fp32);
+    and P rounded to 11 bits keep the output within 1e-3 mean-rel of fp32;
+    heads beyond the f16 range are carried with exact power-of-two factors);
     bf16 keeps the inputs' bits and runs P in bf16, the reference kernel's
     precision class (~1.5e-3 mean-rel). f16 inputs always run in f16."""
     if dtype == torch.float16:
@@ -73,23 +72,13 @@ class DfsCore:
     ``_policy`` and the class-level state dictionaries."""
 
     operand_dtype: Optional[torch.dtype] = None  # None -> operand_dtype_for default
-    # True: f16 operands are checked for values beyond the f16 range (one
-    # device-to-host read per call) and the call is redone on bf16 operands
-    # when any is found; False (default) keeps the call free of host syncs.
-    check_overflow: bool = False
     # The fields a cache entry holds in the reference (attention_wan.py:466-470);
     # get_cache_info counts these per entry, as the reference does (:664-670).
     _entry_fields: Tuple[str, ...] = ("block_mask", "block_indices", "flex_block_mask")
 
     def _prepare(self, q, k, v, perm, layout, pool: bool) -> "ops.Prepared":
-        od = operand_dtype_for(q.dtype, self.operand_dtype)
-        if self.check_overflow and od == torch.float16 and q.dtype == torch.bfloat16:
-            prep = ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=od, pool=pool, check_overflow=True)
-            if int(prep.overflow.item()):
-                logger.warning("DFS attention inputs exceed the f16 range; running this call on bf16 operands")
-                prep = ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=torch.bfloat16, pool=pool)
-            return prep
-        return ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=od, pool=pool)
+        return ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=operand_dtype_for(q.dtype, self.operand_dtype),
+                               pool=pool)
 
     # --- permutation -----------------------------------------------------
     def _device_permutation(self, seq_len: int, device: torch.device) -> torch.Tensor:
@@ -131,22 +120,41 @@ class DfsCore:
             raise RuntimeError("DFS attention runs on a ROCm GPU (HIP kernels); got " + str(q.device))
 
     @staticmethod
-    def _check_cu_seqlens(cu: Optional[torch.Tensor], seq_len: int) -> Optional[int]:
-        """One batch row: cu_seqlens [0, L], [0, L, L] (an empty trailing
-        segment, replace_wan.py:248-249) or [0, valid, L] (a padding segment
-        after the valid tokens, replace_hyvideo.py:221-228). Returns valid
-        when the tensor lives on the host; device tensors are taken as given
-        (the caller passes the valid length separately)."""
-        if cu is None or cu.device.type != "cpu":
-            return None
-        vals = [int(x) for x in cu.flatten().tolist()]
-        ok = vals[0] == 0 and vals[-1] == seq_len and len(vals) in (2, 3) and all(
+    def _host_split(vals, seq_len: int, name: str = "cu_seqlens"):
+        """Host cu_seqlens values checked against the forms the native path
+        runs: None for one whole sequence ([0, L] or [0, L, L]), the values
+        for a split [0, a, L]; anything else raises NotImplementedError."""
+        ok = len(vals) in (2, 3) and vals[0] == 0 and vals[-1] == seq_len and all(
             0 <= a <= b for a, b in zip(vals, vals[1:]))
         if not ok:
             raise NotImplementedError(
-                f"cu_seqlens {vals}: the native DFS path takes one sequence, optionally followed by one "
-                f"padding segment ([0, L], [0, L, L] or [0, valid, L] with L = {seq_len})")
-        return vals[1]
+                f"{name} {vals}: the native DFS path takes one sequence, optionally followed by one more "
+                f"([0, L], [0, L, L] or [0, a, L] with L = {seq_len})")
+        return None if len(vals) == 2 or vals[1] == seq_len else list(vals)
+
+    @staticmethod
+    def _sequences(cu: Optional[torch.Tensor], seq_len: int, device: torch.device,
+                   name: str) -> Optional[torch.Tensor]:
+        """cu_seqlens of one batch row as the device int32 vector the attention
+        kernel reads, or None for one whole sequence. Host tensors are checked
+        here ([0, L], [0, L, L] or [0, a, L] with 0 <= a <= L); device tensors
+        keep their values on the device (no host read) and must hold 2 or 3
+        entries, like the reference's block_sparse_attn_func cu_seqlens of
+        batch 1 or 2 (attention_wan.py:365-386; replace_wan.py:247-250;
+        replace_hyvideo.py:221-228)."""
+        if cu is None:
+            return None
+        if cu.device.type == "cpu":
+            vals = DfsCore._host_split([int(x) for x in cu.flatten().tolist()], seq_len, name)
+            return None if vals is None else ops.device_cu_seqlens(vals, device)
+        if cu.device != device:
+            raise ValueError(f"{name} lives on {cu.device}, the inputs on {device}")
+        flat = cu.reshape(-1)
+        if flat.numel() not in (2, 3):
+            raise NotImplementedError(
+                f"{name} has {flat.numel()} entries: the native DFS path takes one sequence, optionally "
+                "followed by one more")
+        return flat.to(torch.int32).contiguous()
 
     # --- selection and execution --------------------------------------------
     def _select(self, prep: ops.Prepared, layout: ScoringLayout, sparse_ratio: float,
@@ -160,35 +168,15 @@ class DfsCore:
             dict.__setitem__(entry, "block_scores", scores)
         return entry
 
-    def _execute(self, prep: ops.Prepared, entry: MaskEntry, perm: torch.Tensor) -> torch.Tensor:
+    def _execute(self, prep: ops.Prepared, entry: MaskEntry, perm: torch.Tensor,
+                 cu_q: Optional[torch.Tensor] = None, cu_k: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """block_sparse_attn_func of the selected mask (attention_wan.py:335-391,
+        attention_hyvideo.py:1026-1087). With cu_seqlens [0, a, L] the
+        second sequence's rows attend its own keys under the mask indexed from
+        its start, as the external kernel does for the repeated mask; the split
+        is read on the device."""
         return ops.bsa_fwd(prep, entry["row_ptr"], entry["col_idx"], scale=None, out_dtype=prep.dtype,
-                           out_perm=perm)
-
-    def _execute_segments(self, q, k, v, prep: ops.Prepared, entry: MaskEntry, perm: torch.Tensor,
-                          valid: int) -> torch.Tensor:
-        """cu_seqlens [0, valid, L] (attention_hyvideo.py:1054-1082): the
-        external kernel runs the valid tokens and the padding tokens as two
-        sequences, each with the same block mask indexed from its own first
-        token (the mask is repeated per sequence). Valid tokens come first in
-        execution order (the permutation moves video tokens only), so the
-        valid segment is execution rows [0, valid): it runs on the call's own
-        operands and CSR mask, restricted to its leading rows and keys. The
-        padding segment [valid, L) gets its own operands and the mask's
-        leading blocks, without a host round-trip, and its rows are copied
-        into the output."""
-        seq_len = q.shape[2]
-        out = ops.bsa_fwd(prep, entry["row_ptr"], entry["col_idx"], scale=None, out_dtype=prep.dtype,
-                          out_perm=perm, valid_len=valid)
-        n = seq_len - valid
-        nb = math.ceil(n / self.block_size)
-        row_ptr, col_idx = ops.mask_to_csr(entry["block_mask"][:, :nb, :nb].contiguous(), exact=False)
-        seg_perm = (perm[valid:] - valid).contiguous()
-        lay = ScoringLayout(n, n, 16, self.block_size)
-        q_s, k_s, v_s = (x[:, :, valid:] for x in (q, k, v))
-        pad_prep = self._prepare(q_s, k_s, v_s, seg_perm, lay, pool=False)
-        out[:, :, valid:] = ops.bsa_fwd(pad_prep, row_ptr, col_idx, scale=None, out_dtype=prep.dtype,
-                                        out_perm=seg_perm)
-        return out
+                           out_perm=perm, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k)
 
     @staticmethod
     def _tile_counts(entry: MaskEntry) -> np.ndarray:
@@ -208,17 +196,23 @@ class DfsCore:
         cls = type(self)
         self._check_call(q, k, v, attn_mask, causal, drop_rate, batch_size)
         seq_len = q.shape[2]
-        valid_q = self._check_cu_seqlens(cu_seqlens_q, seq_len)
-        valid_kv = self._check_cu_seqlens(cu_seqlens_kv, seq_len)
-        valid = getattr(self, "valid_sequence", None) or valid_q or seq_len
-        if valid_kv is not None and valid_kv != valid:
-            raise NotImplementedError("different query and key segment splits are not supported")
-        if not 0 < valid <= seq_len:
-            raise ValueError(f"valid sequence {valid} outside [1, {seq_len}]")
-        if valid < self._video_len(seq_len):
-            raise ValueError(f"the padding segment starts at {valid}, inside the video "
-                             f"({self._video_len(seq_len)} tokens): only text tokens may be padding")
         device = q.device
+        cu_q = self._sequences(cu_seqlens_q, seq_len, device, "cu_seqlens_q")
+        cu_k = self._sequences(cu_seqlens_kv, seq_len, device, "cu_seqlens_kv")
+        valid = getattr(self, "valid_sequence", None)
+        if cu_q is None and cu_k is None and valid is not None:
+            if not 0 < valid <= seq_len:
+                raise ValueError(f"valid sequence {valid} outside [1, {seq_len}]")
+            if valid < seq_len:
+                cu_q = cu_k = ops.device_cu_seqlens([0, valid, seq_len], device)
+        if (cu_q is None) != (cu_k is None):
+            # One side split, the other whole: the whole side is the first
+            # sequence followed by an empty one.
+            whole = ops.device_cu_seqlens([0, seq_len, seq_len], device)
+            cu_q = whole if cu_q is None else cu_q
+            cu_k = whole if cu_k is None else cu_k
+        if cu_q is not None and cu_q.numel() != cu_k.numel():
+            raise ValueError("cu_seqlens_q and cu_seqlens_kv describe different sequence counts")
         perm = self._device_permutation(seq_len, device)
         layout = self._layout(seq_len)
         key = self._mask_cache_key()
@@ -239,10 +233,7 @@ class DfsCore:
         if cls.record_density:
             self._record_density(entry, seq_len)
         t_att = rec.start(device)
-        if valid < seq_len:
-            out = self._execute_segments(q, k, v, prep, entry, perm, valid)
-        else:
-            out = self._execute(prep, entry, perm)
+        out = self._execute(prep, entry, perm, cu_q, cu_k)
         rec.stop(t_att, phase="attention_execution", step_idx=self.step_idx, layer_idx=self.layer_idx, device=device)
         return out
 

@@ -36,6 +36,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "lds_copy.h"
 
@@ -44,16 +46,21 @@ namespace dfs {
 namespace {
 
 struct BsaParams {
-  // L: valid length (query rows computed, keys attended); R: operand rows per
-  // head; Lo: out / lse rows per head; Qb = Kb = ceil(L / 128); csr_qb: CSR
-  // rows per head (the mask may have been selected over a longer sequence).
-  int H, L, R, Qb, Kb, Lo, csr_qb;
-  int sched;   // workgroup order: 0 head-major across XCDs, 1 XCD-contiguous
-  int rotate;  // rotated key-block sweep (split schedule)
-  int pair_order;  // bitmap-built column order (split schedule, default): by distance from the diagonal
-  int partner;     // ... with the columns shared with the partner row (qb ^ 1) first
+  // L: query rows computed, Lk: keys attended (host values; segment 0 of
+  // device cu_seqlens replaces them per workgroup); R: operand rows per head;
+  // Lo: out / lse rows per head; Qb = ceil(L / 128) sets the grid, Kb =
+  // ceil(Lk / 128); csr_qb: CSR rows per head (the mask may have been
+  // selected over a longer sequence).
+  int H, L, Lk, R, Qb, Kb, Lo, csr_qb;
   float scale_log2;
+  int scale_all;  // 1: every head runs in the scaled instance (f16 q * c may reach 2^15)
   int out_kind;  // 0 bf16, 1 f16, 2 f32
+  // Optional device arrays: cu_q / cu_k, segment offsets in execution order
+  // (segment 0 = [0, cu[1])); exps [3][H], per-head power-of-two exponents
+  // of the f16 operands (q_perm, k_perm, v_t hold x * 2^-e).
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const int32_t* exps;
 };
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -105,27 +112,19 @@ __device__ __forceinline__ float xhalf_sum(float v) {
 
 // (head, query block) of this workgroup; false for a padding slot.
 // Hardware deals workgroup b to XCD b % 8 and each XCD runs its workgroups in
-// increasing b. Head-major mode (default): the i-th workgroup of XCD x takes
-// head h = i / S and query block ((x + h) % 8) * S + i % S (S = ceil(Qb / 8)),
-// so all eight XCDs sweep the same head together: one head's K/V (38.7 MB at
-// 75.6k tokens) stays resident in the shared last-level cache while each
-// XCD's L2 serves neighbouring query blocks. The range an XCD takes rotates
-// with the head, so rows of unequal length (HunyuanVideo's dense text rows
-// at the end of every head) spread over all XCDs instead of one. Mode 1: each XCD owns a contiguous run of
-// (head, query block) pairs instead.
+// increasing b. The i-th workgroup of XCD x takes head h = i / S and query
+// block ((x + h) % 8) * S + i % S (S = ceil(Qb / 8)), so all eight XCDs sweep
+// the same head together: one head's K/V (38.7 MB at 75.6k tokens) stays
+// resident in the shared last-level cache while each XCD's L2 serves
+// neighbouring query blocks. The range an XCD takes rotates with the head,
+// so rows of unequal length (HunyuanVideo's dense text rows at the end of
+// every head) spread over all XCDs instead of one.
 __device__ __forceinline__ bool wg_coords(const BsaParams& p, int& h, int& qb) {
   const int b = blockIdx.x, xcd = b & 7, i = b >> 3;
-  if (p.sched == 0) {
-    const int S = (p.Qb + 7) >> 3;
-    h = i / S;
-    qb = ((xcd + h) & 7) * S + (i - h * S);
-    return qb < p.Qb;
-  }
-  const int nwg = gridDim.x, per = nwg >> 3, rem = nwg & 7;
-  const int id = xcd * per + min(xcd, rem) + i;
-  h = id / p.Qb;
-  qb = id - h * p.Qb;
-  return true;
+  const int S = (p.Qb + 7) >> 3;
+  h = i / S;
+  qb = ((xcd + h) & 7) * S + (i - h * S);
+  return qb < p.Qb;
 }
 
 template <int D, typename QkOp>
@@ -220,19 +219,48 @@ __device__ __forceinline__ void pv_tile(const uint16_t* v_tile, const f32x16* s,
 }
 
 // f16 Q fragments with c = scale * log2(e) folded in (q * c rounded to f16),
-// so that S^T = K (Q c)^T arrives in log2 units.
-template <int D>
+// so that S^T = K (Q c)^T arrives in log2 units. In the SCALED instance the
+// per-head exponents of the f16 operands enter c exactly (q_perm holds
+// q 2^-eq and k_perm k 2^-ek, so c' = c 2^(eq + ek)), and a row whose q * c'
+// would leave the f16 range is stored as q c' 2^-r (r > 0, the smallest
+// power of two that fits): its S arrives as S 2^-r and the kernel multiplies
+// it by row_scale = 2^r. The common instance runs heads without exponents at
+// a scale where |q_perm c| < 2^15 always holds.
+template <int D, bool SCALED>
 __device__ __forceinline__ void load_q_scaled(const uint16_t* __restrict__ q, const BsaParams& p, int h, int qrow,
-                                              int hl, f16x8* qf) {
-  load_q<D, MfmaOp<true>>(q, p, h, qrow, hl, qf);
+                                              int hl, f16x8* qf, float& row_scale) {
+  float c = p.scale_log2;
+  if (SCALED && p.exps) c = ldexpf(c, p.exps[h] + p.exps[p.H + h]);
+  const uint4* src = reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(h) * p.R + qrow) * D);
+  float x[D / 16][8];
+  float mx = 0.f;
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) {
+    const f16x8 v = __builtin_bit_cast(f16x8, src[2 * s + hl]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[s][i] = static_cast<float>(v[i]) * c;
+      if (SCALED) mx = fmaxf(mx, fabsf(x[s][i]));
+    }
+  }
+  float inv = 1.f;
+  row_scale = 1.f;
+  if (SCALED) {
+    mx = xhalf_max(mx);
+    // 2^15 bounds |q c'| after the shift, with room below the f16 maximum.
+    const int r = mx >= 32768.f ? ilogbf(mx) - 14 : 0;
+    inv = ldexpf(1.f, -r);
+    row_scale = ldexpf(1.f, r);
+  }
 #pragma unroll
   for (int s = 0; s < D / 16; ++s)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qf[s][i] = static_cast<_Float16>(static_cast<float>(qf[s][i]) * p.scale_log2);
+    for (int i = 0; i < 8; ++i) qf[s][i] = static_cast<_Float16>(x[s][i] * inv);
 }
 
 // Lazy online softmax on S' = S c - m, where the running reference m enters
-// through the QK MFMA's C input (negm holds -m in every element). On a row's
+// through the QK MFMA's C input (negm holds -m in every element, times qinv
+// = 2^-r for a row whose Q fragments carry 2^-r). On a row's
 // first block m becomes the block maximum; later, m moves only when some row
 // of the wave sees a block maximum above m + kLazyTau, and O and l are
 // rescaled then. The result is the same softmax: numerator and denominator
@@ -241,7 +269,7 @@ __device__ __forceinline__ void load_q_scaled(const uint16_t* __restrict__ q, co
 constexpr float kLazyTau = 8.0f;
 template <int DCH>
 __device__ __forceinline__ void softmax_lazy(f32x16* s, bool first, float& m, float& lsum, f32x16* o,
-                                             f32x16& negm) {
+                                             f32x16& negm, float qinv = 1.f) {
   float mx = -INFINITY;
 #pragma unroll
   for (int kc = 0; kc < 4; ++kc)
@@ -265,7 +293,7 @@ __device__ __forceinline__ void softmax_lazy(f32x16* s, bool first, float& m, fl
     }
     m += shift;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) negm[r] = -m;
+    for (int r = 0; r < 16; ++r) negm[r] = -m * qinv;  // rows stored as Q c 2^-r: the C input is -m 2^-r
   }
 }
 
@@ -360,16 +388,17 @@ __device__ __forceinline__ void make_p(const f32x16* s, f16x8* pf, float& lblk) 
   }
 }
 
-// O = O^T / l for row qrow, columns d = dc*32 + g*8 + hl*4 + (0..3); rows past
-// L are dropped, rows with no kept block give 0.
+// O = O^T / l for row qrow, columns d = dc*32 + g*8 + hl*4 + (0..3), times
+// 2^ev for a V operand stored as v 2^-ev; rows past L are dropped, rows with
+// no kept block give 0.
 template <int D>
-__device__ __forceinline__ void store_out(const BsaParams& p, void* __restrict__ out,
+__device__ __forceinline__ void store_out(const BsaParams& p, int Lq, int ev, void* __restrict__ out,
                                           const int32_t* __restrict__ out_perm, float* __restrict__ lse,
                                           const f32x16* o, float m, float lsum, int h, int qrow, int hl) {
   constexpr int DCH = D / 32;
   const float ltot = xhalf_sum(lsum);
-  const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
-  if (qrow >= p.L) return;
+  const float inv = ltot > 0.f ? ldexpf(1.0f / ltot, ev) : 0.f;  // v_t holds v 2^-ev
+  if (qrow >= Lq) return;
   const int orow = out_perm ? out_perm[qrow] : qrow;
   const int64_t obase = (static_cast<int64_t>(h) * p.Lo + orow) * D;
 #pragma unroll
@@ -395,30 +424,102 @@ __device__ __forceinline__ void store_out(const BsaParams& p, void* __restrict__
     lse[static_cast<int64_t>(h) * p.Lo + qrow] = ltot > 0.f ? (m + log2f(ltot)) * 0.69314718055994531f : -INFINITY;
 }
 
+// Column list of one CSR row into LDS, ordered by distance |c - qb| from the
+// row's own block (c = qb first, then qb - 1, qb + 1, qb - 2, ...). The
+// workgroups resident on an XCD at one time run neighbouring Hilbert query
+// blocks, whose kept columns cluster around their diagonals, so they fetch
+// the same key blocks at about the same time (2% fewer L2 misses than
+// ascending order with the partner row's shared columns first, 0.4-1.2%
+// faster). Columns live in a bitmap at bit 2|c - qb| + (c > qb), compacted in
+// bit order. Columns >= Kb (the keys' blocks) are dropped. bm: W words of
+// LDS scratch, W = (2 Kb + 31) / 32. Every thread of the NT-thread workgroup
+// calls this; it returns the number of columns written to cols.
+template <int NT>
+__device__ int distance_order_cols(int Kb, const int32_t* __restrict__ col_idx, int qb, int beg, int n,
+                                   int32_t* cols, uint32_t* bm, int tid, int w, int lane) {
+  const int W = (2 * Kb + 31) >> 5;
+  for (int i = tid; i < W; i += NT) bm[i] = 0u;
+  block_barrier();
+  for (int i = tid; i < n; i += NT) {
+    const int c = col_idx[beg + i];
+    if (static_cast<unsigned>(c) < static_cast<unsigned>(Kb)) {
+      const int b = 2 * (c >= qb ? c - qb : qb - c) + (c > qb ? 1 : 0);
+      atomicOr(&bm[b >> 5], 1u << (b & 31));
+    }
+  }
+  block_barrier();
+  if (w == 0) {
+    const int per = (W + 63) >> 6;
+    const int w0 = lane * per;
+    int cnt = 0;
+    for (int j = 0; j < per && w0 + j < W; ++j) cnt += __popc(bm[w0 + j]);
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += y;
+    }
+    int pos = incl - cnt;
+    const int total = __shfl(incl, 63, 64);
+    for (int j = 0; j < per && w0 + j < W; ++j) {
+      uint32_t x = bm[w0 + j];
+      while (x) {
+        const int b = (w0 + j) * 32 + __ffs(x) - 1;
+        cols[pos++] = (b & 1) ? qb + (b >> 1) : qb - (b >> 1);
+        x &= x - 1;
+      }
+    }
+    if (lane == 63) bm[0] = static_cast<uint32_t>(total);  // this row's count
+  }
+  block_barrier();
+  const int count = static_cast<int>(bm[0]);
+  block_barrier();  // bm[0] read by everybody before any later LDS write
+  return count;
+}
+
 #define BSA_KERNEL_ARGS                                                                                \
   const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ vt,    \
       const int32_t *__restrict__ row_ptr, const int32_t *__restrict__ col_idx, void *__restrict__ out, \
-      const int32_t *__restrict__ out_perm, float *__restrict__ lse, BsaParams p
+      const int32_t *__restrict__ out_perm, float *__restrict__ lse, BsaParams p_in
 
 // Split schedule: two workgroups per CU, single K and V buffers.
-template <int D, bool QK_F16, bool PV_F16>
-__global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) {
+// Whether head h runs in the scaled instance: its operands carry exponents
+// (Q or K beyond the f16 range), or the scale lets an f16 q * c reach 2^15.
+__device__ __forceinline__ bool head_scaled(const BsaParams& p, int h) {
+  return p.scale_all || (p.exps && (p.exps[h] | p.exps[p.H + h]) != 0);
+}
+
+// One (head, 128-row query block) of the split schedule.
+// VARLEN: segment 0 of device cu_seqlens sets the rows and keys (a separate
+// instance, so the common one keeps the host lengths as kernel arguments).
+// SCALED: rows whose q * c' would leave the f16 range carry 2^-r and S is
+// multiplied back by 2^r (the rare instance, for heads with exponents).
+template <int D, bool QK_F16, bool PV_F16, bool VARLEN, bool SCALED>
+__device__ __forceinline__ void bsa_split_block(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                const uint16_t* __restrict__ vt,
+                                                const int32_t* __restrict__ row_ptr,
+                                                const int32_t* __restrict__ col_idx, void* __restrict__ out,
+                                                const int32_t* __restrict__ out_perm, float* __restrict__ lse,
+                                                const BsaParams& p, int h, int qb, uint16_t* k_lds,
+                                                uint16_t* v_lds, int32_t* cols) {
   constexpr int DCH = D / 32;
   constexpr int K_LOADS = D / 16;  // buffer loads per thread for a K tile
   constexpr int V_LOADS = D / 16;  // ... for a V^T tile (D rows x 256 bytes)
   constexpr uint32_t TILE_BYTES = 128 * D * 2;
   typedef MfmaOp<QK_F16> QkOp;
   typedef MfmaOp<PV_F16> PvOp;
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[128 * D];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * 128];
-  extern __shared__ int32_t cols[];  // kept key blocks of this row (dynamic)
-
-  int h, qb;
-  if (!wg_coords(p, h, qb)) return;
+  // Segment 0 of device cu_seqlens: its query rows and keys (offsets are
+  // trusted, as by the reference's varlen kernel, and clamped to the call).
+  const int Lq = VARLEN ? min(max(p.cu_q[1], 0), p.L) : p.L;
+  const int Lk = VARLEN ? min(max(p.cu_k[1], 0), p.Lk) : p.Lk;
+  const int Kb = (Lk + 127) >> 7;
+  if (qb * 128 >= Lq) return;  // no row of this block is in the segment
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int64_t row = static_cast<int64_t>(h) * p.csr_qb + qb;
   const int beg = row_ptr[row];
-  const int end = beg + min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
+  // A row holds at most as many blocks as the mask has columns (capped by the
+  // call's own key blocks; columns past the segment's keys are dropped below).
+  const int end = beg + min(max(row_ptr[row + 1] - beg, 0), p.Kb);
   const int qrow = qb * 128 + w * 32 + l32;
 
   f32x16 o[DCH];
@@ -438,121 +539,24 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
     const TileCopy<D * 2> kcopy(ws, lane);
     const TileCopy<256> vcopy(ws, lane);
     typename QkOp::vec qf[D / 16];
+    float row_scale = 1.f;  // 2^r of a row whose Q fragments carry 2^-r (SCALED)
     if constexpr (QK_F16)
-      load_q_scaled<D>(q, p, h, qrow, hl, qf);
+      load_q_scaled<D, SCALED>(q, p, h, qrow, hl, qf, row_scale);
     else
       load_q<D, QkOp>(q, p, h, qrow, hl, qf);
-    f32x16 negm = f32x16{};  // -m in every element (f16 Q/K)
+    const float qinv = 1.f / row_scale;
+    f32x16 negm = f32x16{};  // -m (times 2^-r) in every element (f16 Q/K)
     // Column list of this row into LDS (read back with uniform ds_reads), and
     // Q fragments forced complete here so no wait for them lands in the loop.
-    int n = end - beg;
-    if (p.pair_order) {
-      // Diagonal-distance order: the row's columns by distance |c - qb| from
-      // its own block (c = qb first, then qb - 1, qb + 1, qb - 2, ...). The
-      // workgroups resident on an XCD at one time run neighbouring Hilbert
-      // query blocks, whose kept columns cluster around their diagonals, so
-      // they fetch the same key blocks at about the same time (2% fewer L2
-      // misses than ascending partner-first order, 0.4-1.2% faster). Columns
-      // live in a bitmap at bit 2|c - qb| + (c > qb), compacted in bit order.
-      // With partner set, the columns shared with the partner row (query
-      // block qb ^ 1) come first, each group in distance order.
-      const int W = (2 * p.Kb + 31) >> 5;
-      auto bpos = [&](int c) { return 2 * (c >= qb ? c - qb : qb - c) + (c > qb ? 1 : 0); };
-      uint32_t* bm = reinterpret_cast<uint32_t*>(cols + p.Kb);  // [own W][partner W]
-      for (int i = tid; i < 2 * W; i += 256) bm[i] = 0u;
-      block_barrier();
-      for (int i = tid; i < n; i += 256) {
-        const int c = col_idx[beg + i];
-        if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) {
-          const int b = bpos(c);
-          atomicOr(&bm[b >> 5], 1u << (b & 31));
-        }
-      }
-      const int qp = qb ^ 1;
-      if (p.partner && qp < p.Qb) {
-        const int64_t prow = static_cast<int64_t>(h) * p.csr_qb + qp;
-        const int pbeg = row_ptr[prow];
-        const int pn = min(max(row_ptr[prow + 1] - pbeg, 0), p.Kb);
-        for (int i = tid; i < pn; i += 256) {
-          const int c = col_idx[pbeg + i];
-          if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) {
-            const int b = bpos(c);
-            atomicOr(&bm[W + (b >> 5)], 1u << (b & 31));
-          }
-        }
-      }
-      block_barrier();
-      if (w == 0) {
-        const int per = (W + 63) >> 6;
-        const int w0 = lane * per;
-        int cs = 0, co = 0;
-        for (int j = 0; j < per && w0 + j < W; ++j) {
-          cs += __popc(bm[w0 + j] & bm[W + w0 + j]);
-          co += __popc(bm[w0 + j] & ~bm[W + w0 + j]);
-        }
-        int is = cs, io = co;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const int ys = __shfl_up(is, off, 64), yo = __shfl_up(io, off, 64);
-          if (lane >= off) {
-            is += ys;
-            io += yo;
-          }
-        }
-        const int n_shared = __shfl(is, 63, 64);
-        int ps = is - cs, po = n_shared + io - co;
-        for (int j = 0; j < per && w0 + j < W; ++j) {
-          const uint32_t own = bm[w0 + j], par = bm[W + w0 + j];
-          uint32_t x = own & par;
-          while (x) {
-            const int b = (w0 + j) * 32 + __ffs(x) - 1;
-            cols[ps++] = (b & 1) ? qb + (b >> 1) : qb - (b >> 1);
-            x &= x - 1;
-          }
-          x = own & ~par;
-          while (x) {
-            const int b = (w0 + j) * 32 + __ffs(x) - 1;
-            cols[po++] = (b & 1) ? qb + (b >> 1) : qb - (b >> 1);
-            x &= x - 1;
-          }
-        }
-        if (lane == 63) bm[0] = static_cast<uint32_t>(n_shared + io);  // this row's count
-      }
-      block_barrier();
-      n = static_cast<int>(bm[0]);
-      block_barrier();  // bm[0] read by everybody before any later LDS write
-    } else {
-      for (int i = tid; i < n; i += 256) cols[i] = col_idx[beg + i];
-    }
+    const int n = distance_order_cols<256>(Kb, col_idx, qb, beg, end - beg, cols,
+                                           reinterpret_cast<uint32_t*>(cols + p.Kb), tid, w, lane);
 #pragma unroll
     for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qf[s]));
     block_barrier();
-    // Rotated sweep: the i-th workgroup of an XCD starts at the first kept
-    // column >= i * Kb / CONC (CONC = workgroups resident per XCD) and wraps
-    // around. Workgroups start 1 / CONC of a sweep apart, so at any moment the
-    // resident workgroups of an XCD work on neighbouring key blocks and share
-    // them in L2. The order is a fixed function of the workgroup, so results
-    // are deterministic.
-    int j0 = 0;
-    if (p.rotate && !p.pair_order) {
-      constexpr int CONC = 64;  // 32 CUs per XCD x 2 workgroups per CU
-      const int start = static_cast<int>((static_cast<int64_t>(blockIdx.x >> 3) * p.Kb / CONC) % p.Kb);
-      int lo = 0, hi = n;  // lower_bound(cols, start)
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (cols[mid] < start) lo = mid + 1; else hi = mid;
-      }
-      j0 = lo == n ? 0 : lo;
-    }
-    auto col_at = [&](int t) -> int {
-      int j = j0 + t;
-      j = j >= n ? j - n : j;
-      return __builtin_amdgcn_readfirstlane(cols[j]);
-    };
+    auto col_at = [&](int t) -> int { return __builtin_amdgcn_readfirstlane(cols[t]); };
     int kb = col_at(0);
     kcopy.template issue<K_LOADS>(krs, kb * TILE_BYTES, k_base, ws);
     vcopy.template issue<V_LOADS>(vrs, kb * TILE_BYTES, v_base, ws);
-    const bool tail_possible = (p.L & 127) != 0;
 
     for (int t = 0; t < n; ++t) {
       // After the last block the copies reload the current block into the
@@ -569,12 +573,18 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
         __builtin_amdgcn_s_setprio(1);
         qk_tile_ahead<D>(k_lds, qf, l32, hl, s, negm);
         __builtin_amdgcn_s_setprio(0);
+        if constexpr (SCALED) {  // rows whose q c' exceeds the f16 range carry 2^-r
+#pragma unroll
+          for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[kc][r] *= row_scale;
+        }
       } else
         qk_tile<D, QkOp>(k_lds, qf, l32, hl, s);
       block_barrier();  // K tile fully consumed
       kcopy.template issue<K_LOADS>(krs, kb_next * TILE_BYTES, k_base, ws);
-      if (tail_possible && kb == p.Kb - 1) {
-        int valid = p.L - kb * 128;
+      if ((Lk & 127) != 0 && kb == (Lk >> 7)) {  // the keys' last block is partial
+        int valid = Lk & 127;
         asm volatile("" : "+s"(valid));  // compares stay in this (rare) branch
         mask_tail(s, valid, hl);
       }
@@ -584,12 +594,12 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
         // accepted unless it overflows f16 (some S - m >= 16, which turns
         // the block's row sum inf); only then is the block redone with a
         // moved reference. P <= 2^16 keeps f16's 11-bit precision.
-        if (t == 0) softmax_lazy<DCH>(s, true, m, lsum, o, negm);
+        if (t == 0) softmax_lazy<DCH>(s, true, m, lsum, o, negm, qinv);
         f16x8 pf[8];
         float lblk;
         make_p(s, pf, lblk);
         if (t > 0 && __any(!(lblk < INFINITY))) {
-          softmax_lazy<DCH>(s, false, m, lsum, o, negm);
+          softmax_lazy<DCH>(s, false, m, lsum, o, negm, qinv);
           make_p(s, pf, lblk);
         }
         lsum += lblk;
@@ -597,7 +607,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
         block_barrier();
         pv_tile_regs<D>(v_lds, pf, o, l32, hl);
       } else if constexpr (QK_F16) {
-        softmax_lazy<DCH>(s, t == 0, m, lsum, o, negm);
+        softmax_lazy<DCH>(s, t == 0, m, lsum, o, negm, qinv);
         wait_vmcnt<K_LOADS>();
         block_barrier();
         pv_tile_log2<D, PvOp>(v_lds, s, lsum, o, l32, hl);
@@ -613,20 +623,34 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) 
     }
     wait_vmcnt_0();  // the trailing copies have landed before the workgroup's LDS is released
   }
-  store_out<D>(p, out, out_perm, lse, o, m, lsum, h, qrow, hl);
+  store_out<D>(p, VARLEN ? min(max(p.cu_q[1], 0), p.L) : p.L, p.exps ? p.exps[2 * p.H + h] : 0, out, out_perm,
+               lse, o, m, lsum, h, qrow, hl);
 }
 
-// (head, pair of query blocks) of an eight-wave workgroup; head-major across
-// XCDs with the per-head rotation of wg_coords.
-
-template <int G>
-__device__ __forceinline__ bool group_coords(const BsaParams& p, int& h, int& grp) {
-  const int groups = (p.Qb + G - 1) / G;
-  const int b = blockIdx.x, xcd = b & 7, i = b >> 3;
-  const int S = (groups + 7) >> 3;
-  h = i / S;
-  grp = ((xcd + h) & 7) * S + (i - h * S);
-  return grp < groups;
+template <int D, bool QK_F16, bool PV_F16, bool VARLEN, bool SCALED>
+__global__ void __launch_bounds__(256, 2) bsa_fwd_split_kernel(BSA_KERNEL_ARGS) {
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[128 * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * 128];
+  extern __shared__ int32_t cols[];  // kept key blocks of this row (dynamic)
+  if constexpr (!SCALED) {
+    // Common instance: one workgroup per (head, query block), XCD-aware.
+    int h, qb;
+    if (!wg_coords(p_in, h, qb)) return;
+    if (QK_F16 && head_scaled(p_in, h)) return;  // the scaled instance's head
+    bsa_split_block<D, QK_F16, PV_F16, VARLEN, false>(q, k, vt, row_ptr, col_idx, out, out_perm, lse, p_in, h, qb,
+                                                      k_lds, v_lds, cols);
+  } else {
+    // Scaled instance: a small grid (x: workgroups per head, y: head) whose
+    // workgroups walk the query blocks of the heads that carry exponents and
+    // exit at once for every other head.
+    const int h = blockIdx.y;
+    if (!head_scaled(p_in, h)) return;
+    for (int qb = blockIdx.x; qb < p_in.Qb; qb += gridDim.x) {
+      block_barrier();  // the previous block's LDS reads are done
+      bsa_split_block<D, QK_F16, PV_F16, VARLEN, true>(q, k, vt, row_ptr, col_idx, out, out_perm, lse, p_in, h, qb,
+                                                       k_lds, v_lds, cols);
+    }
+  }
 }
 
 struct BsaArgs {
@@ -637,281 +661,162 @@ struct BsaArgs {
   float* lse;
 };
 
-// Softmax of one block for the ping-pong schedule, in two halves. S (log2
-// units, from the prescaled Q) arrives without the running reference; the
-// first half takes the block maximum, moves the reference m lazily (when a
-// row's maximum exceeds m + kLazyTau, or on the row's first block) rescaling
-// O and l, and forms P = exp2(S - m) for keys 0-63; the second half forms P
-// for keys 64-127. P (f16, the PV operand order) stays in registers until the
-// next MFMA phase. The VALU work of this phase overlaps the other group's
-// MFMAs, so the subtraction costs little and saves the 16 registers a C
-// input would hold.
-template <int DCH>
-__device__ __forceinline__ void pp_softmax_first(const f32x16* s, bool first, float& m, float& lsum, f32x16* o,
-                                                 f16x8* pf) {
-  typedef MfmaOp<true> Op;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int kc = 0; kc < 4; ++kc)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kc][r]);
-  const float bm = xhalf_max(mx);
-  if (first || __any(bm > m + kLazyTau)) {
-    float mnew = first ? bm : fmaxf(bm, m);
-    if (!(mnew > -INFINITY)) mnew = m;  // a row with every key masked keeps m
-    if (!first) {
-      const float alpha = exp2_fast(m - mnew);
-      lsum *= alpha;
-#pragma unroll
-      for (int i = 0; i < DCH; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-    }
-    m = mnew;
-  }
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    Op::pair pr[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      pr[j] = Op::pack(exp2_fast(s[ks >> 1][(ks & 1) * 8 + 2 * j] - m),
-                       exp2_fast(s[ks >> 1][(ks & 1) * 8 + 2 * j + 1] - m));
-      lsum = Op::sum2(pr[j], lsum);
-    }
-    pf[ks] = __builtin_bit_cast(f16x8, pr);
-  }
+struct SegParams {
+  int H, L, R, csr_qb, Lo;
+  int qk_f16, pv_f16, out_kind;
+  float scale_log2;
+  const int32_t* cu_q;  // [n_seq + 1] (device)
+  const int32_t* cu_k;
+  int n_seq;
+  const int32_t* exps;  // optional [3][H]
+};
+
+__device__ __forceinline__ float operand_at(const uint16_t* base, int64_t i, bool f16) {
+  return f16 ? f16_bits_to_f32(base[i]) : bf16_bits_to_f32(base[i]);
 }
 
-__device__ __forceinline__ void pp_softmax_second(const f32x16* s, float m, float& lsum, f16x8* pf) {
-  typedef MfmaOp<true> Op;
-#pragma unroll
-  for (int ks = 4; ks < 8; ++ks) {
-    Op::pair pr[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      pr[j] = Op::pack(exp2_fast(s[ks >> 1][(ks & 1) * 8 + 2 * j] - m),
-                       exp2_fast(s[ks >> 1][(ks & 1) * 8 + 2 * j + 1] - m));
-      lsum = Op::sum2(pr[j], lsum);
-    }
-    pf[ks] = __builtin_bit_cast(f16x8, pr);
-  }
-}
-
-
-// Ping-pong schedule (f16 operands). One workgroup of eight
-// waves per CU serves two adjacent query blocks of a head: waves 0-3 (group
-// 0) run block 2i, waves 4-7 (group 1) block 2i+1, each group with its own K
-// and V buffers and its own column list (the columns both rows keep first, in
-// the same order, so the second fetch of a shared key block hits L2). Each
-// group alternates an MFMA phase (PV of block k-1, then QK^T of block k) with
-// a VALU phase (softmax of block k), and the groups run half a cycle apart:
-// every SIMD holds one wave of each group, so one wave's exponentials issue
-// while the other's MFMAs run. Every phase has two workgroup barriers (mid,
-// end), the same number for all waves, which keeps the groups in step.
-// Copies: V(k) is issued at the mid barrier of MFMA phase k (after PV(k-1)
-// left the V buffer) and K(k+1) at the start of VALU phase k (after QK^T(k)
-// left the K buffer); each lands at least one and a half phases before use.
-// A group past its last block issues no copies and keeps taking part in the
-// barriers until the other group is done.
+// The rows of a call after segment 0 of cu_seqlens, in fp32 (one wave per
+// row, keys one by one with an exact running maximum). For n_seq == 2 the
+// rows [cq1, cq2) attend keys [ck1, ck2) under the same block mask indexed
+// from each segment's own start (query block (r - cq1) / 128 selects the CSR
+// row, key block j covers keys ck1 + 128 j ..), as the reference's varlen
+// kernel treats the second sequence of its batch (attention_hyvideo.py:
+// 1054-1082, the mask repeated per sequence at :359). Rows outside every
+// query segment are zero (lse -inf). Sized for short padding segments (a few
+// hundred tokens of text padding); the work grows with rows x kept keys.
 template <int D>
-__global__ void __launch_bounds__(512, 1) bsa_fwd_pp_kernel(BSA_KERNEL_ARGS) {
-  constexpr int DCH = D / 32;
-  constexpr int LOADS = D / 16;  // 16-byte loads per thread for one tile (4 waves)
-  constexpr uint32_t TILE_BYTES = 128 * D * 2;
-  constexpr uint16_t NONE = 0xFFFFu;
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][128 * D];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * 128];
-  __shared__ int n_rows[2];
-  extern __shared__ uint32_t dyn[];  // bitmaps [2][W], then columns [2][Kb] (uint16)
-
-  int h, grp;
-  if (!group_coords<2>(p, h, grp)) return;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
-  const int g = __builtin_amdgcn_readfirstlane(w >> 2), rg = __builtin_amdgcn_readfirstlane(w & 3);
-  const int W = (p.Kb + 31) >> 5;
-  uint32_t* bm = dyn;
-  uint16_t* cols = reinterpret_cast<uint16_t*>(dyn + 2 * W);  // [2][Kb]
-
-  for (int i = tid; i < 2 * W; i += 512) bm[i] = 0u;
-  block_barrier();
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int qr = grp * 2 + r;
-    if (qr < p.Qb) {
-      const int64_t row = static_cast<int64_t>(h) * p.csr_qb + qr;
-      const int beg = row_ptr[row];
-      const int cnt = min(max(row_ptr[row + 1] - beg, 0), p.Kb);  // a row holds at most Kb blocks
-      for (int i = tid; i < cnt; i += 512) {
-        const int c = col_idx[beg + i];
-        if (static_cast<unsigned>(c) < static_cast<unsigned>(p.Kb)) atomicOr(&bm[r * W + (c >> 5)], 1u << (c & 31));
-      }
-    }
+__global__ void __launch_bounds__(256) bsa_segment_kernel(const uint16_t* __restrict__ q,
+                                                          const uint16_t* __restrict__ k,
+                                                          const uint16_t* __restrict__ vt,
+                                                          const int32_t* __restrict__ row_ptr,
+                                                          const int32_t* __restrict__ col_idx,
+                                                          void* __restrict__ out, const int32_t* __restrict__ out_perm,
+                                                          float* __restrict__ lse, SegParams p) {
+  constexpr int DPL = D / 64;  // head dims per lane
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), n_waves = gridDim.x * 4;
+  const int cq1 = min(max(p.cu_q[1], 0), p.L);
+  const int cq2 = p.n_seq == 2 ? min(max(p.cu_q[2], cq1), p.L) : cq1;
+  const int ck1 = p.n_seq == 2 ? min(max(p.cu_k[1], 0), p.L) : 0;
+  const int ck2 = p.n_seq == 2 ? min(max(p.cu_k[2], ck1), p.L) : 0;
+  const int seg_kb = (ck2 - ck1 + 127) >> 7;
+  const bool qk16 = p.qk_f16 != 0, pv16 = p.pv_f16 != 0;
+  float sq = p.scale_log2, sv = 1.f;
+  if (p.exps) {
+    sq = ldexpf(sq, p.exps[h] + p.exps[p.H + h]);
+    sv = ldexpf(1.f, p.exps[2 * p.H + h]);
   }
-  block_barrier();
-  if (w == 0) {
-    // Row r's list: the shared columns ascending, then its own ascending.
-    const int per = (W + 63) >> 6;
-    const int w0 = lane * per;
-    int cs = 0, ca = 0, cb = 0;
-    for (int j = 0; j < per && w0 + j < W; ++j) {
-      const uint32_t a = bm[w0 + j], b = bm[W + w0 + j];
-      cs += __popc(a & b);
-      ca += __popc(a & ~b);
-      cb += __popc(b & ~a);
-    }
-    int is = cs, ia = ca, ib = cb;
+  const int64_t hq = static_cast<int64_t>(h) * p.R * D;
+  for (int r = cq1 + wave; r < p.L; r += n_waves) {
+    float o[DPL];
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int ys = __shfl_up(is, off, 64), ya = __shfl_up(ia, off, 64), yb = __shfl_up(ib, off, 64);
-      if (lane >= off) {
-        is += ys;
-        ia += ya;
-        ib += yb;
+    for (int j = 0; j < DPL; ++j) o[j] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    if (r < cq2 && seg_kb > 0) {
+      float qv[DPL];
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) qv[j] = operand_at(q, hq + static_cast<int64_t>(r) * D + lane * DPL + j, qk16) * sq;
+      const int64_t crow = static_cast<int64_t>(h) * p.csr_qb + ((r - cq1) >> 7);
+      const int beg = row_ptr[crow], end = row_ptr[crow + 1];
+      for (int idx = beg; idx < end; ++idx) {
+        const int cb = col_idx[idx];
+        if (cb < 0 || cb >= seg_kb) continue;
+        const int k0 = ck1 + cb * 128, k1 = min(k0 + 128, ck2);
+        for (int key = k0; key < k1; key += 4) {
+          float s[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            float part = 0.f;
+            if (key + u < k1) {
+#pragma unroll
+              for (int j = 0; j < DPL; ++j)
+                part += qv[j] * operand_at(k, hq + static_cast<int64_t>(key + u) * D + lane * DPL + j, qk16);
+            }
+            s[u] = part;
+          }
+#pragma unroll
+          for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) s[u] += __shfl_xor(s[u], off, 64);
+          float mx = m;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (key + u >= k1) s[u] = -INFINITY;
+            mx = fmaxf(mx, s[u]);
+          }
+          const float alpha = exp2_fast(m - mx);
+          l *= alpha;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) o[j] *= alpha;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (key + u >= k1) continue;
+            const float pu = exp2_fast(s[u] - mx);
+            l += pu;
+            const int t = key + u, tb = t & 127;
+            const int slot = (tb & ~15) | ((tb & 3) | ((tb & 4) << 1) | ((tb & 8) >> 1));  // swap23 (an involution)
+            const int64_t vb = (static_cast<int64_t>(h) * (p.R / 128) + (t >> 7)) * D * 128;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) o[j] += pu * operand_at(vt, vb + static_cast<int64_t>(lane * DPL + j) * 128 + slot, pv16);
+          }
+          m = mx;
+        }
       }
     }
-    const int n_shared = __shfl(is, 63, 64);
-    int ps = is - cs, pa = n_shared + ia - ca, pb = n_shared + ib - cb;
-    for (int j = 0; j < per && w0 + j < W; ++j) {
-      const uint32_t a = bm[w0 + j], b = bm[W + w0 + j];
-      uint32_t x = a & b;
-      while (x) {
-        const uint16_t c = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
-        x &= x - 1;
-        cols[ps] = c;
-        cols[p.Kb + ps] = c;
-        ++ps;
-      }
-      x = a & ~b;
-      while (x) {
-        cols[pa++] = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
-        x &= x - 1;
-      }
-      x = b & ~a;
-      while (x) {
-        cols[p.Kb + pb++] = static_cast<uint16_t>((w0 + j) * 32 + __ffs(x) - 1);
-        x &= x - 1;
-      }
+    const float inv = l > 0.f ? sv / l : 0.f;
+    const int orow = out_perm ? out_perm[r] : r;
+    const int64_t ob = (static_cast<int64_t>(h) * p.Lo + orow) * D + lane * DPL;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const float v = o[j] * inv;
+      if (p.out_kind == DFS_DTYPE_F32)
+        static_cast<float*>(out)[ob + j] = v;
+      else if (p.out_kind == DFS_DTYPE_BF16)
+        static_cast<uint16_t*>(out)[ob + j] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+      else
+        static_cast<uint16_t*>(out)[ob + j] = static_cast<uint16_t>(f32_to_f16_bits(v));
     }
-    if (lane == 63) {
-      n_rows[0] = n_shared + ia;
-      n_rows[1] = n_shared + ib;
-    }
+    if (lse && lane == 0)
+      lse[static_cast<int64_t>(h) * p.Lo + r] = l > 0.f ? (m + log2f(l)) * 0.69314718055994531f : -INFINITY;
   }
-  block_barrier();
-  const int qb = grp * 2 + g;
-  const int n = qb < p.Qb ? n_rows[g] : 0;
-  const int n_all = max(grp * 2 < p.Qb ? n_rows[0] : 0, grp * 2 + 1 < p.Qb ? n_rows[1] : 0);
-  const uint16_t* my_cols = cols + g * p.Kb;
-  (void)NONE;
-
-  f32x16 o[DCH];
-#pragma unroll
-  for (int i = 0; i < DCH; ++i) o[i] = f32x16{};
-  float m = 0.f, lsum = 0.f;
-  f16x8 qf[D / 16];
-  const int qrow = qb * 128 + rg * 32 + l32;
-  if (n > 0) load_q_scaled<D>(q, p, h, qrow, hl, qf);
-
-  const uint32_t head_bytes = static_cast<uint32_t>(p.R) * D * 2;
-  const auto krs = make_rsrc(k + static_cast<int64_t>(h) * p.R * D, head_bytes);
-  const auto vrs = make_rsrc(vt + static_cast<int64_t>(h) * p.R * D, head_bytes);
-  void* const k_base = k_lds[g];
-  void* const v_base = v_lds[g];
-  const TileCopy<D * 2> kcopy(rg, lane);
-  const TileCopy<256> vcopy(rg, lane);
-  auto col_at = [&](int t) -> int { return t < n ? __builtin_amdgcn_readfirstlane(my_cols[t]) : p.Kb; };
-  const bool tail_possible = (p.L & 127) != 0;
-#pragma unroll
-  for (int s2 = 0; s2 < D / 16; ++s2) asm volatile("" ::"v"(qf[s2]));
-
-  if (g == 0 && n > 0) kcopy.template issue<LOADS>(krs, col_at(0) * TILE_BYTES, k_base, rg);  // group 1: in V(-1)
-  f32x16 s[4];
-  f16x8 pf[8];
-  // MFMA phase kk: PV(kk-1) from the P registers, then QK^T(kk) into s.
-  auto mfma_phase = [&](int kk) {
-    if (kk >= 1 && kk - 1 < n) {
-      __builtin_amdgcn_s_setprio(1);
-      pv_tile_regs<D>(v_lds[g], pf, o, l32, hl);
-      __builtin_amdgcn_s_setprio(0);
-    }
-    wait_vmcnt_0();  // K(kk) landed
-    block_barrier();
-    const int kb = col_at(kk);
-    if (kk < n) vcopy.template issue<LOADS>(vrs, kb * TILE_BYTES, v_base, rg);
-    if (kk < n) {
-      __builtin_amdgcn_s_setprio(1);
-      qk_tile_ahead<D>(k_lds[g], qf, l32, hl, s);
-      __builtin_amdgcn_s_setprio(0);
-      if (tail_possible && kb == p.Kb - 1) {
-        int valid = p.L - kb * 128;
-        asm volatile("" : "+s"(valid));  // compares stay in this (rare) branch
-        mask_tail(s, valid, hl);
-      }
-    }
-    block_barrier();
-  };
-  // VALU phase kk: softmax of block kk into the P registers.
-  auto valu_phase = [&](int kk) {
-    const bool more = kk + 1 < n;
-    if (more) kcopy.template issue<LOADS>(krs, col_at(kk + 1) * TILE_BYTES, k_base, rg);
-    if (kk >= 0 && kk < n) pp_softmax_first<DCH>(s, kk == 0, m, lsum, o, pf);
-    block_barrier();
-    if (kk >= 0 && kk < n) pp_softmax_second(s, m, lsum, pf);
-    // V(kk) landed; K(kk+1), issued after it, may still be in flight (loads
-    // complete in issue order). Without a K copy behind it, wait for all.
-    if (more) wait_vmcnt<LOADS>(); else wait_vmcnt_0();
-    block_barrier();
-  };
-  // Group 0 runs M(i) V(i), group 1 V(i-1) M(i): the same four barriers per
-  // iteration, half a cycle apart. Group 1's V(-1) only waits.
-  if (g == 0) {
-    for (int i = 0; i <= n_all; ++i) {
-      mfma_phase(i);
-      valu_phase(i);
-    }
-  } else {
-    for (int i = 0; i <= n_all; ++i) {
-      valu_phase(i - 1);
-      mfma_phase(i);
-    }
-  }
-  if (qb < p.Qb) store_out<D>(p, out, out_perm, lse, o, m, lsum, h, qrow, hl);
 }
 
-enum BsaSchedule { kSplit = 0, kPingPong = 1 };
-
-template <int D>
-void launch_pp(const BsaArgs& a, const BsaParams& p, hipStream_t s) {
-  const int groups = (p.Qb + 1) / 2, S = (groups + 7) / 8;
-  const int W = (p.Kb + 31) / 32;
-  const size_t smem = static_cast<size_t>(2 * W) * sizeof(uint32_t) + static_cast<size_t>(2 * p.Kb) * 2;
-  bsa_fwd_pp_kernel<D><<<dim3(static_cast<unsigned>(8 * S * p.H)), 512, smem, s>>>(
-      a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out, a.out_perm, a.lse, p);
+template <int D, bool QK_F16, bool PV_F16, bool VARLEN>
+void launch_split_as(const BsaArgs& a, const BsaParams& p, hipStream_t s) {
+  const size_t smem = static_cast<size_t>(p.Kb) * sizeof(int32_t) +
+                      static_cast<size_t>((2 * p.Kb + 31) / 32) * sizeof(uint32_t);
+  if (!p.scale_all) {
+    const int S = (p.Qb + 7) / 8;
+    bsa_fwd_split_kernel<D, QK_F16, PV_F16, VARLEN, false><<<dim3(static_cast<unsigned>(8 * S * p.H)), 256, smem, s>>>(
+        a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out, a.out_perm, a.lse, p);
+  }
+  if constexpr (QK_F16) {
+    // Heads with exponents (only when some bf16 input exceeds the f16 range)
+    // or every head (large scales): a few workgroups per head.
+    if (p.exps || p.scale_all) {
+      const unsigned per_head = p.scale_all ? static_cast<unsigned>(p.Qb) : 8u;
+      bsa_fwd_split_kernel<D, QK_F16, PV_F16, VARLEN, true>
+          <<<dim3(per_head, static_cast<unsigned>(p.H)), 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
+                                                                     a.out_perm, a.lse, p);
+    }
+  }
 }
 
 template <int D, bool QK_F16, bool PV_F16>
-void launch_typed(const BsaArgs& a, const BsaParams& p, BsaSchedule sched, hipStream_t s) {
-  // The ping-pong schedule needs f16 operands and keeps 4 tiles (128 KB at
-  // D = 128) plus two uint16 column lists in LDS: it runs up to 4096 key
-  // blocks; beyond, and for bf16 operands, the split schedule runs.
-  if constexpr (QK_F16 && PV_F16)
-    if (sched == kPingPong && p.Kb <= 4096) return launch_pp<D>(a, p, s);
-  const int S = (p.Qb + 7) / 8;
-  dim3 grid(static_cast<unsigned>(p.sched == 0 ? 8 * S * p.H : p.H * p.Qb));
-  const size_t smem = static_cast<size_t>(p.Kb) * sizeof(int32_t) +
-                      (p.pair_order ? static_cast<size_t>(2 * ((2 * p.Kb + 31) / 32)) * sizeof(uint32_t) : 0);
-  bsa_fwd_split_kernel<D, QK_F16, PV_F16><<<grid, 256, smem, s>>>(a.q, a.k, a.vt, a.row_ptr, a.col_idx, a.out,
-                                                                 a.out_perm, a.lse, p);
+void launch_split(const BsaArgs& a, const BsaParams& p, hipStream_t s) {
+  if (p.cu_q) return launch_split_as<D, QK_F16, PV_F16, true>(a, p, s);
+  launch_split_as<D, QK_F16, PV_F16, false>(a, p, s);
 }
 
 template <int D>
-void launch_bsa(const BsaArgs& a, const BsaParams& p, bool qk_f16, bool pv_f16, BsaSchedule sched, hipStream_t s) {
+void launch_bsa(const BsaArgs& a, const BsaParams& p, bool qk_f16, bool pv_f16, hipStream_t s) {
   if (qk_f16)
-    launch_typed<D, true, true>(a, p, sched, s);
+    launch_split<D, true, true>(a, p, s);
   else if (pv_f16)
-    launch_typed<D, false, true>(a, p, sched, s);
+    launch_split<D, false, true>(a, p, s);
   else
-    launch_typed<D, false, false>(a, p, sched, s);
+    launch_split<D, false, false>(a, p, s);
 }
 
 }  // namespace
@@ -921,7 +826,8 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
                            const int32_t* row_ptr, const int32_t* col_idx, int64_t heads,
                            int64_t seq_len, int64_t head_dim, int dtype, int pv_dtype, float scale,
                            void* out, int out_dtype, const int32_t* out_perm, float* lse,
-                           int64_t valid_len, dfs_stream_t stream) {
+                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t n_seq,
+                           const int32_t* exps, dfs_stream_t stream) {
   using namespace dfs;
   const char* name = "dfs_bsa_fwd";
   DFS_REQUIRE(q_perm && k_perm && v_t && row_ptr && col_idx && out, "%s: NULL operand", name);
@@ -941,42 +847,56 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   // LDS: 64 KB of tiles (split schedule) plus the row's column list.
   DFS_REQUIRE(qb <= 8192, "%s: %lld key blocks exceed the LDS column list", name, (long long)qb);
   DFS_REQUIRE(scale > 0.f && isfinite(scale), "%s: scale must be positive and finite", name);
-  if (valid_len == 0) valid_len = seq_len;
-  DFS_REQUIRE(valid_len > 0 && valid_len <= seq_len, "%s: valid_len=%lld outside [1, %lld]", name,
-              (long long)valid_len, (long long)seq_len);
-  const int64_t vb = (valid_len + kBlock - 1) / kBlock;
+  DFS_REQUIRE(n_seq == 1 || n_seq == 2, "%s: n_seq=%lld (supported: 1 or 2 sequences)", name, (long long)n_seq);
+  DFS_REQUIRE((cu_seqlens_q == nullptr) == (cu_seqlens_k == nullptr),
+              "%s: pass both cu_seqlens_q and cu_seqlens_k or neither", name);
+  DFS_REQUIRE(n_seq == 1 || cu_seqlens_q, "%s: two sequences need cu_seqlens", name);
   BsaArgs a{static_cast<const uint16_t*>(q_perm), static_cast<const uint16_t*>(k_perm),
             static_cast<const uint16_t*>(v_t), row_ptr, col_idx, out, out_perm, lse};
   BsaParams p{};
   p.H = static_cast<int>(heads);
-  p.L = static_cast<int>(valid_len);
+  p.L = p.Lk = static_cast<int>(seq_len);
   p.R = static_cast<int>(qb * kBlock);
-  p.Qb = static_cast<int>(vb);
-  p.Kb = static_cast<int>(vb);
+  p.Qb = p.Kb = static_cast<int>(qb);
   p.Lo = static_cast<int>(seq_len);
   p.csr_qb = static_cast<int>(qb);
   p.scale_log2 = scale * 1.4426950408889634f;
+  // An f16 operand is below 65504 < 2^16, so q * c stays below 2^15 unless
+  // c >= 0.5 (a softmax scale >= 0.35); then every head takes the scaled
+  // instance, whose rows carry their own powers of two.
+  p.scale_all = (dtype == DFS_DTYPE_F16 && p.scale_log2 >= 0.5f) ? 1 : 0;
   p.out_kind = out_dtype;
-  const char* order = getenv("DFSATTN_AMD_BSA_SCHED");
-  p.sched = (order && order[0] == '1') ? 1 : 0;
-  const char* po = getenv("DFSATTN_AMD_BSA_ORDER");
-  // DFSATTN_AMD_BSA_ORDER: unset (default, diagonal-distance order), "pair"
-  // (partner-shared columns first, then the rest, each by distance) or
-  // "rotate" (each row's own ascending list from a workgroup-dependent start).
-  // A valid length below seq_len needs the bitmap orders, which drop columns >= Kb.
-  p.pair_order = (po && strcmp(po, "rotate") == 0 && valid_len == seq_len) ? 0 : 1;
-  p.partner = (po && strcmp(po, "pair") == 0) ? 1 : 0;
-  const char* rot = getenv("DFSATTN_AMD_BSA_ROTATE");
-  p.rotate = (rot && rot[0] == '0') ? 0 : 1;
-  const char* kern = getenv("DFSATTN_AMD_BSA_KERNEL");
-  // DFSATTN_AMD_BSA_KERNEL: "split" (default) or "pp" (ping-pong, f16
-  // operands; split otherwise).
-  const BsaSchedule sched = (kern && strcmp(kern, "pp") == 0) ? kPingPong : kSplit;
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.exps = exps;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool qk_f16 = dtype == DFS_DTYPE_F16, pv_f16 = pv_dtype == DFS_DTYPE_F16;
   if (head_dim == 128)
-    launch_bsa<128>(a, p, qk_f16, pv_f16, sched, s);
+    launch_bsa<128>(a, p, qk_f16, pv_f16, s);
   else
-    launch_bsa<64>(a, p, qk_f16, pv_f16, sched, s);
+    launch_bsa<64>(a, p, qk_f16, pv_f16, s);
+  if (cu_seqlens_q) {
+    SegParams sp{};
+    sp.H = p.H;
+    sp.L = p.L;
+    sp.R = p.R;
+    sp.csr_qb = p.csr_qb;
+    sp.Lo = p.Lo;
+    sp.qk_f16 = qk_f16;
+    sp.pv_f16 = pv_f16;
+    sp.out_kind = out_dtype;
+    sp.scale_log2 = p.scale_log2;
+    sp.cu_q = cu_seqlens_q;
+    sp.cu_k = cu_seqlens_k;
+    sp.n_seq = static_cast<int>(n_seq);
+    sp.exps = exps;
+    // Enough waves for a few hundred rows per head; each wave strides over
+    // the rows after segment 0.
+    const dim3 grid(16, static_cast<unsigned>(heads));
+    if (head_dim == 128)
+      bsa_segment_kernel<128><<<grid, 256, 0, s>>>(a.q, a.k, a.vt, row_ptr, col_idx, out, out_perm, lse, sp);
+    else
+      bsa_segment_kernel<64><<<grid, 256, 0, s>>>(a.q, a.k, a.vt, row_ptr, col_idx, out, out_perm, lse, sp);
+  }
   return check_launch(name);
 }

@@ -103,7 +103,7 @@ struct PrepParams {
   uint4* q_lo;
   uint4* k_hi;  // [H][k_tiles][D] bf16
   uint4* k_lo;
-  int32_t* v_overflow;
+  int32_t* flags;  // optional [3][H] overflow flags (Q, K, V)
   int L;         // tokens
   int Lv;        // video tokens (== L for Wan)
   int R;         // execution rows per head, ceil(L/128)*128
@@ -181,7 +181,7 @@ __global__ void __launch_bounds__(256) prep_qk_kernel(PrepParams p) {
       add_chunk(acc, val, p.in_f16 != 0);  // tile means of the input values
     }
   }
-  if (p.v_overflow && overflow) atomicOr(p.v_overflow, 1);
+  if (p.flags && overflow) atomicOr(&p.flags[(is_k ? 1 : 0) * gridDim.y + h], 1);
   const int n_tiles = is_k ? p.k_tiles : p.q_tiles;
   if (!p.pool || t >= n_tiles) return;
 #pragma unroll
@@ -253,7 +253,89 @@ __global__ void __launch_bounds__(16 * (D / 8)) prep_v_kernel(PrepParams p) {
     dst[d * (kBlock / 8) + kg] =
         make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
   }
-  if (p.v_overflow && overflow) atomicOr(p.v_overflow, 1);
+  if (p.flags && overflow) atomicOr(&p.flags[2 * gridDim.y + h], 1);
+}
+
+// bf16 -> f16 of eight packed values times sc (a power of two).
+__device__ __forceinline__ uint4 bf16x8_to_f16x8_scaled(const uint4& v, float sc) {
+  uint32_t e[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) e[i] = f32_to_f16_bits(bf16_bits_to_f32(u16_at(v, i)) * sc);
+  return make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+}
+
+// One workgroup per (head, tensor) of a call whose bf16 inputs were rounded
+// to f16 operands. When the prepare kernel flagged the head (a finite value
+// beyond the f16 range), the head's operand is rewritten from the inputs as
+// x * 2^-e, with e >= 1 the smallest exponent that brings the head's largest
+// finite |x| below 2^15, and exps[tensor][h] = e; otherwise exps[tensor][h] =
+// 0. The flag is cleared. Powers of two are exact, so the attention kernel
+// folds 2^e back into its Q prescale (Q, K) and its output scale (V).
+template <int D>
+__global__ void __launch_bounds__(1024) prep_fixup_kernel(PrepParams p, int32_t* flags, int32_t* exps) {
+  constexpr int CPR = D / 8;
+  const int h = blockIdx.x, t = blockIdx.y, H = gridDim.x;
+  const int slot = t * H + h;
+  if (flags[slot] == 0) {
+    if (threadIdx.x == 0) exps[slot] = 0;
+    return;
+  }
+  const uint4* src = (t == 0 ? p.q : t == 1 ? p.k : p.v) + static_cast<int64_t>(h) * p.L * CPR;
+  const int n = p.L * CPR;
+  float mx = 0.f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const uint4 v = src[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = fabsf(bf16_bits_to_f32(u16_at(v, e)));
+      if (f < INFINITY) mx = fmaxf(mx, f);  // infinities and NaN stay as they are
+    }
+  }
+  __shared__ float red[16];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = 0.f;
+  for (int i = 0; i < static_cast<int>(blockDim.x >> 6); ++i) mx = fmaxf(mx, red[i]);
+  const int e = mx >= 32768.f ? max(1, ilogbf(mx) - 14) : 1;
+  const float sc = ldexpf(1.f, -e);
+  if (t < 2) {
+    uint4* dst = (t == 0 ? p.q_perm : p.k_perm) + static_cast<int64_t>(h) * p.R * CPR;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int x = i / CPR, c = i - x * CPR;
+      const int s = p.perm[x];
+      const uint4 val = (s >= 0 && s < p.L) ? src[static_cast<int64_t>(s) * CPR + c] : make_uint4(0, 0, 0, 0);
+      dst[static_cast<int64_t>(x) * CPR + c] = bf16x8_to_f16x8_scaled(val, sc);
+    }
+  } else {
+    // v_t: per 128-token block [D][128] with swap23 slot order; one 16-byte
+    // chunk = 8 slots of one head dim.
+    const uint16_t* vs = reinterpret_cast<const uint16_t*>(src);
+    uint4* dst = p.v_t + static_cast<int64_t>(h) * (p.R / kBlock) * D * (kBlock / 8);
+    const int chunks = (p.R / kBlock) * D * (kBlock / 8);
+    for (int i = threadIdx.x; i < chunks; i += blockDim.x) {
+      const int blk = i / (D * 16), rem = i - blk * (D * 16), d = rem >> 4, kg = rem & 15;
+      uint32_t bits[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int phys = kg * 8 + j;
+        const int tok = blk * kBlock + (phys & ~15) + swap23(phys & 15);
+        float f = 0.f;
+        if (tok < p.L) {
+          const int s = p.perm[tok];
+          if (s >= 0 && s < p.L) f = bf16_bits_to_f32(vs[static_cast<int64_t>(s) * D + d]);
+        }
+        bits[j] = f32_to_f16_bits(f * sc);
+      }
+      dst[i] = make_uint4(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16), bits[4] | (bits[5] << 16),
+                          bits[6] | (bits[7] << 16));
+    }
+  }
+  if (threadIdx.x == 0) {
+    exps[slot] = e;
+    flags[slot] = 0;
+  }
 }
 
 }  // namespace
@@ -279,7 +361,7 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* 
                     int64_t heads, int64_t seq_len, int64_t head_dim, int dtype,
                     int64_t video_len, int64_t tile_size, int operand_dtype, void* q_perm,
                     void* k_perm, void* v_t, uint16_t* q_pool_hi, uint16_t* q_pool_lo,
-                    uint16_t* k_pool_hi, uint16_t* k_pool_lo, int32_t* v_overflow,
+                    uint16_t* k_pool_hi, uint16_t* k_pool_lo, int32_t* overflow,
                     dfs_stream_t stream) {
   using namespace dfs;
   DFS_REQUIRE(q && k && v && perm && q_perm && k_perm && v_t, "dfs_prepare_qkv: NULL operand");
@@ -322,7 +404,7 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* 
   p.q_lo = reinterpret_cast<uint4*>(q_pool_lo);
   p.k_hi = reinterpret_cast<uint4*>(k_pool_hi);
   p.k_lo = reinterpret_cast<uint4*>(k_pool_lo);
-  p.v_overflow = v_overflow;
+  p.flags = overflow;
   p.L = static_cast<int>(seq_len);
   p.Lv = static_cast<int>(video_len);
   p.R = static_cast<int>(kb * kBlock);
@@ -345,6 +427,37 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* 
     prep_v_kernel<64><<<gv, 16 * 8, 0, s>>>(p);
   }
   return check_launch("dfs_prepare_qkv");
+}
+
+int dfs_prepare_fixup(const void* q, const void* k, const void* v, const int32_t* perm, int64_t heads,
+                      int64_t seq_len, int64_t head_dim, void* q_perm, void* k_perm, void* v_t,
+                      int32_t* overflow, int32_t* exps, dfs_stream_t stream) {
+  using namespace dfs;
+  DFS_REQUIRE(q && k && v && perm && q_perm && k_perm && v_t && overflow && exps, "dfs_prepare_fixup: NULL operand");
+  DFS_REQUIRE(head_dim == 64 || head_dim == 128, "dfs_prepare_fixup: head_dim=%lld (supported: 64, 128)",
+              (long long)head_dim);
+  DFS_REQUIRE(heads > 0 && heads < 65536, "dfs_prepare_fixup: heads=%lld out of range", (long long)heads);
+  DFS_REQUIRE(seq_len > 0, "dfs_prepare_fixup: seq_len=%lld", (long long)seq_len);
+  const int64_t kb = (seq_len + kBlock - 1) / kBlock;
+  DFS_REQUIRE(kb * kBlock * head_dim < (int64_t(1) << 31),
+              "dfs_prepare_fixup: seq_len=%lld too long for 32-bit per-head indexing", (long long)seq_len);
+  PrepParams p{};
+  p.q = static_cast<const uint4*>(q);
+  p.k = static_cast<const uint4*>(k);
+  p.v = static_cast<const uint4*>(v);
+  p.perm = perm;
+  p.q_perm = static_cast<uint4*>(q_perm);
+  p.k_perm = static_cast<uint4*>(k_perm);
+  p.v_t = static_cast<uint4*>(v_t);
+  p.L = static_cast<int>(seq_len);
+  p.R = static_cast<int>(kb * kBlock);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(heads), 3);
+  if (head_dim == 128)
+    prep_fixup_kernel<128><<<grid, 1024, 0, s>>>(p, overflow, exps);
+  else
+    prep_fixup_kernel<64><<<grid, 1024, 0, s>>>(p, overflow, exps);
+  return check_launch("dfs_prepare_fixup");
 }
 
 }  // extern "C"

@@ -9,7 +9,7 @@ from __future__ import annotations
 import ctypes
 import math
 from dataclasses import dataclass
-from typing import Optional, Tuple
+from typing import Dict, Optional, Sequence, Tuple
 
 import torch
 
@@ -121,17 +121,21 @@ class Prepared:
     q_lo: Optional[torch.Tensor] = None
     k_hi: Optional[torch.Tensor] = None  # [H, k_tiles, D] bf16
     k_lo: Optional[torch.Tensor] = None
-    overflow: Optional[torch.Tensor] = None
+    # int32 [3, H] power-of-two exponents of the f16 operands (q_perm, k_perm
+    # and v_t hold x * 2^-e for heads whose bf16 inputs exceed the f16 range);
+    # None when the operands keep the inputs' dtype.
+    exps: Optional[torch.Tensor] = None
 
 
 def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.Tensor,
-                layout: ScoringLayout, operand_dtype: Optional[torch.dtype] = None, pool: bool = True,
-                check_overflow: bool = False) -> Prepared:
+                layout: ScoringLayout, operand_dtype: Optional[torch.dtype] = None, pool: bool = True) -> Prepared:
     """Gathers Q, K, V into execution order (V block-transposed) and, with
     ``pool``, writes the tile means used for scoring. ``operand_dtype`` (f16
     by default) is the dtype of the attention operands: f16 rounds bf16
-    inputs to f16; bf16 keeps their bits. ``check_overflow`` allocates a flag
-    set when a finite input exceeds the f16 range."""
+    inputs to f16; bf16 keeps their bits. With f16 operands from bf16 inputs
+    every finite input is kept: a head whose values exceed the f16 range is
+    stored scaled by an exact power of two (``Prepared.exps``), decided and
+    applied on the device without a host round trip."""
     _require_device(q, k, v, perm)
     _require_int32(perm=perm)
     heads, length, dim = _heads_rows(q)
@@ -160,12 +164,16 @@ def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.T
         prep.q_lo = torch.empty_like(prep.q_hi)
         prep.k_hi = torch.empty((heads, layout.k_tiles, dim), dtype=torch.bfloat16, device=dev)
         prep.k_lo = torch.empty_like(prep.k_hi)
-    if check_overflow:
-        prep.overflow = torch.zeros(1, dtype=torch.int32, device=dev)
+    rounds = q.dtype == torch.bfloat16 and operand_dtype == torch.float16
+    flags = torch.zeros(3 * heads, dtype=torch.int32, device=dev) if rounds else None
     _lib.call("dfs_prepare_qkv", _ptr(q), _ptr(k), _ptr(v), _ptr(perm), heads, length, dim,
               DTYPE_CODE[q.dtype], layout.video_len, layout.tile, DTYPE_CODE[operand_dtype],
               _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(prep.q_hi), _ptr(prep.q_lo),
-              _ptr(prep.k_hi), _ptr(prep.k_lo), _ptr(prep.overflow), _stream(q))
+              _ptr(prep.k_hi), _ptr(prep.k_lo), _ptr(flags), _stream(q))
+    if rounds:
+        prep.exps = torch.empty((3, heads), dtype=torch.int32, device=dev)
+        _lib.call("dfs_prepare_fixup", _ptr(q), _ptr(k), _ptr(v), _ptr(perm), heads, length, dim,
+                  _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(flags), _ptr(prep.exps), _stream(q))
     return prep
 
 
@@ -232,22 +240,41 @@ def topk_from_scores(scores: torch.Tensor, policy: TopkPolicy, row_ptr: torch.Te
     return col_idx, mask
 
 
+def _check_cu(cu: torch.Tensor, name: str, device: torch.device) -> int:
+    """A device int32 cu_seqlens vector of 2 or 3 entries; returns n_seq."""
+    if cu.device != device or cu.dtype != torch.int32 or not cu.is_contiguous() or cu.dim() != 1:
+        raise ValueError(f"{name} must be a contiguous int32 vector on {device}")
+    if cu.numel() not in (2, 3):
+        raise NotImplementedError(
+            f"{name} has {cu.numel()} entries: the native DFS path runs one sequence, optionally "
+            "followed by one more (cu_seqlens [0, L], [0, L, L] or [0, a, L])")
+    return cu.numel() - 1
+
+
 def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale: Optional[float] = None,
             out_dtype: Optional[torch.dtype] = None, out_perm: Optional[torch.Tensor] = None,
-            want_lse: bool = False, out: Optional[torch.Tensor] = None, valid_len: Optional[int] = None):
+            want_lse: bool = False, out: Optional[torch.Tensor] = None,
+            cu_seqlens_q: Optional[torch.Tensor] = None, cu_seqlens_k: Optional[torch.Tensor] = None):
     """Block-sparse attention over the CSR mask. Returns out [1, H, L, D] —
     original token order when ``out_perm`` is given, execution order otherwise —
     and the fp32 log-sum-exp [H, L] (execution order) when ``want_lse``.
-    ``valid_len`` < L restricts the call to the first valid_len execution
-    rows and keys (the mask's leading blocks; rows from valid_len on are not
-    written)."""
-    _require_device(prep.q_perm, row_ptr, col_idx, out_perm, out)
+    ``cu_seqlens_q`` / ``cu_seqlens_k`` (device int32, 2 or 3 entries, both
+    or neither) split the call into sequences as the reference's varlen
+    kernel does: sequence i's queries [cq[i], cq[i+1]) attend its keys
+    [ck[i], ck[i+1]) under the mask indexed from each sequence's start; rows
+    in no query sequence are zero. The offsets stay on the device."""
+    _require_device(prep.q_perm, row_ptr, col_idx, out_perm, out, cu_seqlens_q, cu_seqlens_k)
     _require_int32(row_ptr=row_ptr, col_idx=col_idx, out_perm=out_perm)
     if row_ptr.numel() != prep.heads * prep.layout.q_blocks + 1:
         raise ValueError(f"row_ptr has {row_ptr.numel()} entries for {prep.heads} x {prep.layout.q_blocks} rows")
+    if (cu_seqlens_q is None) != (cu_seqlens_k is None):
+        raise ValueError("pass both cu_seqlens_q and cu_seqlens_k or neither")
+    n_seq = 1
+    if cu_seqlens_q is not None:
+        n_seq = _check_cu(cu_seqlens_q, "cu_seqlens_q", prep.q_perm.device)
+        if _check_cu(cu_seqlens_k, "cu_seqlens_k", prep.q_perm.device) != n_seq:
+            raise ValueError("cu_seqlens_q and cu_seqlens_k describe different sequence counts")
     L = prep.layout.seq_len
-    if valid_len is not None and not 0 < valid_len <= L:
-        raise ValueError(f"valid_len {valid_len} outside [1, {L}]")
     out_dtype = out_dtype or prep.dtype
     if out is None:
         out = torch.empty((1, prep.heads, L, prep.head_dim), dtype=out_dtype, device=prep.q_perm.device)
@@ -258,8 +285,23 @@ def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale:
     _lib.call("dfs_bsa_fwd", _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(row_ptr),
               _ptr(col_idx), prep.heads, L, prep.head_dim, DTYPE_CODE[prep.operand_dtype],
               DTYPE_CODE[prep.operand_dtype], scale, _ptr(out), DTYPE_CODE[out_dtype], _ptr(out_perm),
-              _ptr(lse), int(valid_len or 0), _stream(prep.q_perm))
+              _ptr(lse), _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), n_seq, _ptr(prep.exps), _stream(prep.q_perm))
     return (out, lse) if want_lse else out
+
+
+_CU_CACHE: Dict[Tuple[Tuple[int, ...], str], torch.Tensor] = {}
+
+
+def device_cu_seqlens(values: Sequence[int], device: torch.device) -> torch.Tensor:
+    """Device int32 copy of host cu_seqlens values, cached per (values,
+    device) and copied from pinned memory without waiting for the device."""
+    key = (tuple(int(x) for x in values), str(device))
+    t = _CU_CACHE.get(key)
+    if t is None:
+        host = torch.tensor(key[0], dtype=torch.int32).pin_memory()
+        t = host.to(device, non_blocking=True)
+        _CU_CACHE[key] = t
+    return t
 
 
 def mask_to_csr(mask: torch.Tensor, exact: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -157,10 +157,12 @@ class HunyuanVideo_DFSAttn_Processor2_0:
 
     @staticmethod
     def get_cu_max_seqlen(attention_mask: torch.Tensor, device):
-        """[0, valid, total] for queries and keys (replace_hyvideo.py:221-228)."""
-        valid = attention_mask.sum()
+        """[0, valid, total] for queries and keys (replace_hyvideo.py:221-228),
+        built on the mask's device: the valid count never visits the host."""
         total = attention_mask.numel()
-        cu = torch.tensor([0, int(valid), total], dtype=torch.int32, device=device)
+        cu = torch.full((3,), total, dtype=torch.int32, device=device)
+        cu[0] = 0
+        cu[1] = attention_mask.reshape(-1).sum(dtype=torch.int32).to(device)
         return cu, cu.clone(), total, total
 
     def _dump_attention_debug(self, query, key, value, sparse_output, dense_output, valid_sequence):
@@ -263,14 +265,14 @@ class HunyuanVideo_DFSAttn_Processor2_0:
                 max_seqlen_kv=max_kv, sparse_execution=self.sparse_execution, hybrid_threshold=self.hybrid_threshold,
                 block_top_p=self.block_top_p, token_top_k=self.token_top_k,
                 residual_candidate_blocks=self.residual_candidate_blocks, selector_mode=self.selector_mode,
-                fine_top_p=self.fine_top_p, flashinfer64_valid_sequence=int(cu_q[1].item()), **self.flashinfer64)
+                fine_top_p=self.fine_top_p, **self.flashinfer64)
         else:
             full_mode = "flash" if mode == "dense" else mode
             start = DFS_Attention.timing_recorder.start(query.device)
             hidden_states = full_attention(query, key, value, mode=full_mode, drop_rate=0.0,
                                            attn_mask=attention_mask, causal=False, cu_seqlens_q=cu_q,
                                            cu_seqlens_kv=cu_kv, max_seqlen_q=max_q, max_seqlen_kv=max_kv,
-                                           batch_size=query.shape[0])
+                                           batch_size=query.shape[0], operand_dtype=DFS_Attention.operand_dtype)
             DFS_Attention.timing_recorder.stop(start, phase="attention_execution", step_idx=self.step_idx,
                                                layer_idx=self.layer_idx, device=query.device)
 

@@ -24,6 +24,7 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
+from .attention_wan import DFS_Attention as WanDFSAttention
 from .attention_wan import dfs_attention
 from .fullattention import full_attention
 
@@ -185,8 +186,12 @@ class Wan_DFSAttn_Processor2_0:
         _, _, s_q, _ = query.shape
         s_k_total = key.shape[2]
         s_k = int(attention_mask.sum().item()) if attention_mask is not None else s_k_total
-        cu_seqlens_q = torch.tensor([0, s_q, s_q], dtype=torch.int32, device=query.device)
-        cu_seqlens_kv = torch.tensor([0, s_k, s_k_total], dtype=torch.int32, device=query.device)
+        # The reference builds these on the device (replace_wan.py:247-250);
+        # their values are host integers here, so host tensors carry them and
+        # no per-call synchronous copy is made (the attention paths move a
+        # real split to the device themselves).
+        cu_seqlens_q = torch.tensor([0, s_q, s_q], dtype=torch.int32)
+        cu_seqlens_kv = torch.tensor([0, s_k, s_k_total], dtype=torch.int32)
 
         if self.branch() == "dfs":
             hidden_states = dfs_attention(
@@ -202,7 +207,7 @@ class Wan_DFSAttn_Processor2_0:
             hidden_states = full_attention(
                 query, key, value, mode="flash", drop_rate=0.0, attn_mask=attention_mask, causal=False,
                 cu_seqlens_q=cu_seqlens_q, cu_seqlens_kv=cu_seqlens_kv, max_seqlen_q=s_q, max_seqlen_kv=s_k_total,
-                batch_size=query.shape[0])
+                batch_size=query.shape[0], operand_dtype=WanDFSAttention.operand_dtype)
 
         hidden_states = hidden_states.transpose(1, 2).flatten(2, 3).type_as(query)
         if hidden_states_img is not None:

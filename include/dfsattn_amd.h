@@ -39,7 +39,8 @@ enum { DFS_DTYPE_BF16 = 0, DFS_DTYPE_F16 = 1, DFS_DTYPE_F32 = 2 };
 /* Last error message of the calling thread ("" if none). */
 const char* dfs_last_error(void);
 
-/* ABI version; bumped whenever a signature below changes (2: scoring workspace, attention valid_len). */
+/* ABI version; bumped whenever a signature below changes (2: scoring workspace; 3: device cu_seqlens
+ * and per-head operand exponents in the attention call, per-head overflow flags and dfs_prepare_fixup). */
 int dfs_abi_version(void);
 
 /*
@@ -87,8 +88,10 @@ int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst,
  *   q_pool_*     [H][ceil(video_len/128)*128/tile][D] (may all be NULL to skip
  *   k_pool_*     [H][ceil(L/128)*128/tile][D]          pooling: cached steps).
  *                Means of the input values, whatever operand_dtype.
- *   overflow     optional int32 flag, set to 1 when bf16 inputs are rounded
- *                to f16 and some |q|, |k| or |v| exceeds the f16 range.
+ *   overflow     optional int32 [3][H] flags (Q, K, V per head), zeroed by
+ *                the caller; entry [t][h] is set when bf16 inputs are
+ *                rounded to f16 and a finite value of tensor t, head h
+ *                exceeds the f16 range. Pass them to dfs_prepare_fixup.
  * Replaces the q/k/v gathers of attention_wan.py:173-174, 338-340 and the
  * padding + tile means of attention_wan.py:176-205.
  */
@@ -100,6 +103,22 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v,
                     uint16_t* q_pool_hi, uint16_t* q_pool_lo,
                     uint16_t* k_pool_hi, uint16_t* k_pool_lo,
                     int32_t* overflow, dfs_stream_t stream);
+
+/*
+ * Completes dfs_prepare_qkv for bf16 inputs with f16 operands so that every
+ * finite input is represented: for each flagged (tensor, head) it rewrites
+ * that head's q_perm, k_perm or v_t from the inputs as x * 2^-e (e >= 1, the
+ * smallest exponent that brings the head's largest finite |x| below 2^15)
+ * and sets exps[t][h] = e; every other entry of exps ([3][H] int32) is set
+ * to 0, and the flags are cleared. dfs_bsa_fwd takes exps and undoes the
+ * factors exactly (powers of two). Heads within the f16 range cost one flag
+ * read. No reference counterpart: the reference's kernel computes in bf16
+ * (block_sparse_attn_func, attention_wan.py:379-386), whose range this keeps.
+ */
+int dfs_prepare_fixup(const void* q, const void* k, const void* v,
+                      const int32_t* perm, int64_t heads, int64_t seq_len,
+                      int64_t head_dim, void* q_perm, void* k_perm, void* v_t,
+                      int32_t* overflow, int32_t* exps, dfs_stream_t stream);
 
 /*
  * Hierarchical block scoring and top-k in one kernel: pooled QK^T * D^-1/2
@@ -167,32 +186,44 @@ int dfs_topk_from_scores(const float* scores, int64_t heads,
  *                        of q_perm and k_perm, pv_dtype that of v_t (f16/f16
  *                        and bf16/bf16 as prepared; bf16/f16 also accepted).
  *                        With f16 q_perm the kernel folds scale * log2(e)
- *                        into Q, rounding Q * scale * log2(e) to f16.
+ *                        into Q, rounding Q * scale * log2(e) to f16 (a row
+ *                        beyond the f16 range is carried with an exact
+ *                        power-of-two factor).
  *   scale                softmax scale (the reference passes None -> D^-1/2).
  *   out                  out_dtype 0/1/2; when out_perm is NULL, out is
  *                        [H][L][D] in execution order; otherwise row i is
  *                        written to out[h][out_perm[i]] (fused unpermute).
  *   lse                  optional fp32 [H][L] natural-log sum-exp (execution
  *                        order).
- *   valid_len            0 (or L): the whole sequence. 0 < valid_len < L: only
- *                        execution rows and keys below valid_len take part
- *                        (columns >= ceil(valid_len/128) of the CSR rows are
- *                        skipped; rows from valid_len on are not written): the
- *                        first of the two sequences of cu_seqlens [0, valid, L]
- *                        (attention_hyvideo.py:1054-1082), run on the whole
- *                        call's operands and mask. CSR columns must ascend.
- * Keys >= valid_len in the last block are masked out; rows with no kept
- * block give 0.
+ *   cu_seqlens_q/_k      optional device int32 [n_seq + 1] offsets of the
+ *                        query and key sequences in execution order (both
+ *                        or neither; n_seq 1 or 2). Sequence i: queries
+ *                        [cq[i], cq[i+1]) attend keys [ck[i], ck[i+1])
+ *                        under the block mask indexed from each sequence's
+ *                        own start (the mask repeated per sequence); rows in
+ *                        no query sequence are zero. Offsets are read on the
+ *                        device (no host synchronisation) and trusted, as by
+ *                        the reference's varlen kernel, clamped to [0, L].
+ *                        Sequence 0 runs on the MFMA kernel, sequence 1 on
+ *                        an fp32 kernel sized for short padding segments.
+ *                        Without them: one sequence of L tokens.
+ *   exps                 optional int32 [3][H] per-head exponents written by
+ *                        dfs_prepare_fixup (q_perm, k_perm, v_t hold
+ *                        x * 2^-e); NULL means all zero.
+ * Keys past a sequence's end in its last block are masked out; rows with no
+ * kept block give 0. CSR columns must ascend.
  * Replaces block_sparse_attn_func (attention_wan.py:379-386;
- * attention_hyvideo.py:1075-1082) and, with out_perm, the final inverse
- * gather (attention_wan.py:390).
+ * attention_hyvideo.py:1075-1082), including its cu_seqlens_q /
+ * cu_seqlens_k arguments, and, with out_perm, the final inverse gather
+ * (attention_wan.py:390).
  */
 int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v_t,
                 const int32_t* row_ptr, const int32_t* col_idx,
                 int64_t heads, int64_t seq_len, int64_t head_dim, int dtype,
                 int pv_dtype, float scale, void* out, int out_dtype,
-                const int32_t* out_perm, float* lse, int64_t valid_len,
-                dfs_stream_t stream);
+                const int32_t* out_perm, float* lse,
+                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                int64_t n_seq, const int32_t* exps, dfs_stream_t stream);
 
 /* uint8/bool block mask [H][Qb][Kb] -> per-row counts int32 [H*Qb].
  * Part of the bool-mask interface of block_sparse_attn_func

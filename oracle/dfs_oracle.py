@@ -423,6 +423,37 @@ def masked_attention(q_perm: torch.Tensor, k_perm: torch.Tensor, v_perm: torch.T
     return out
 
 
+def varlen_attention(q_perm: torch.Tensor, k_perm: torch.Tensor, v_perm: torch.Tensor, mask: torch.Tensor,
+                     cu_q, cu_k, block: int = BLOCK, scale: Optional[float] = None) -> torch.Tensor:
+    """block_sparse_attn_func's varlen semantics (attention_wan.py:359-386,
+    attention_hyvideo.py:1054-1082): sequence i's queries [cq[i], cq[i+1])
+    attend its keys [ck[i], ck[i+1]) under mask[h, a, b], where a and b count
+    128-token blocks from the sequence's own first query and first key (the
+    reference repeats ``base_blockmask`` per sequence). Rows in no query
+    sequence, and sequences without keys, give zero."""
+    q, k, v = q_perm.float(), k_perm.float(), v_perm.float()
+    _, n_heads, _, dim = q.shape
+    scale = 1.0 / math.sqrt(dim) if scale is None else scale
+    out = torch.zeros_like(q)
+    bq = [int(x) for x in cu_q]
+    bk = [int(x) for x in cu_k]
+    for (q0, q1), (k0, k1) in zip(zip(bq, bq[1:]), zip(bk, bk[1:])):
+        nq, nk = q1 - q0, k1 - k0
+        if nq <= 0 or nk <= 0:
+            continue
+        nkb = math.ceil(nk / block)
+        for h in range(n_heads):
+            for a in range(math.ceil(nq / block)):
+                cols = torch.nonzero(mask[h, a, :nkb]).flatten().tolist()
+                if not cols:
+                    continue
+                tok = torch.cat([torch.arange(k0 + c * block, min(k0 + (c + 1) * block, k1)) for c in cols])
+                rows = slice(q0 + a * block, min(q0 + (a + 1) * block, q1))
+                p = torch.softmax((q[0, h, rows] @ k[0, h, tok].T) * scale, dim=-1)
+                out[0, h, rows] = p @ v[0, h, tok]
+    return out
+
+
 def segment_attention(q_perm: torch.Tensor, k_perm: torch.Tensor, v_perm: torch.Tensor,
                       mask: torch.Tensor, cu_seqlens, block: int = BLOCK) -> torch.Tensor:
     """Varlen block-masked attention (attention_hyvideo.py:1054-1082): each

@@ -1,6 +1,8 @@
 """End-to-end parity of the reference-compatible API on the GPU:
 dfs_attention (Wan and HunyuanVideo variants) against the CPU oracle's whole
 call on the same (bf16-rounded) inputs, and the mask cache behaviour."""
+import math
+
 import pytest
 import torch
 
@@ -118,15 +120,22 @@ def test_api_rejects_what_the_native_path_cannot_run(dev):
         dfs_attention(q.float(), q.float(), q.float(), step_idx=100, layer_idx=7, tile_size=16)
     with pytest.raises(ValueError):
         hy_dfs(q, q, q, step_idx=30, layer_idx=2, tile_size=16, video_len=200, block_top_p=0.9)
-    with pytest.raises(ValueError):  # padding may only cover text tokens
-        hy_dfs(q, q, q, step_idx=30, layer_idx=3, tile_size=16, video_len=200, flashinfer64_valid_sequence=150)
     cu = torch.tensor([0, 100, 200, 256], dtype=torch.int32)
-    with pytest.raises(NotImplementedError):  # more than one padding segment
+    with pytest.raises(NotImplementedError):  # more than two sequences
         hy_dfs(q, q, q, step_idx=30, layer_idx=4, tile_size=16, video_len=200, cu_seqlens_q=cu, cu_seqlens_kv=cu)
+    with pytest.raises(NotImplementedError):  # ... also on the device (only the entry count is checked there)
+        hy_dfs(q, q, q, step_idx=30, layer_idx=4, tile_size=16, video_len=200, cu_seqlens_q=cu.to(dev),
+               cu_seqlens_kv=cu.to(dev))
+    with pytest.raises(ValueError):  # different sequence counts for queries and keys
+        hy_dfs(q, q, q, step_idx=30, layer_idx=4, tile_size=16, video_len=200,
+               cu_seqlens_q=torch.tensor([0, 100, 256], dtype=torch.int32, device=dev),
+               cu_seqlens_kv=torch.tensor([0, 256], dtype=torch.int32, device=dev) + 0)
 
 
 @pytest.mark.parametrize("grid,text_len,pad,via", [((3, 16, 20), 100, 40, "valid"), ((4, 16, 16), 300, 230, "cu"),
-                                                    ((4, 16, 16), 300, 172, "valid")])
+                                                    ((4, 16, 16), 300, 172, "valid"), ((3, 16, 20), 100, 40, "device"),
+                                                    ((4, 16, 16), 300, 230, "device"),
+                                                    ((3, 16, 20), 100, 400, "device")])
 def test_hunyuan_padding_segment_matches_oracle(dev, grid, text_len, pad, via):
     """cu_seqlens [0, valid, L] (text padding, replace_hyvideo.py:221-228):
     the mask is selected over the whole sequence, then the valid tokens and
@@ -144,8 +153,12 @@ def test_hunyuan_padding_segment_matches_oracle(dev, grid, text_len, pad, via):
     L, vl = cfg.seq_len, cfg.video_len
     valid = L - pad
     cu = torch.tensor([0, valid, L], dtype=torch.int32)
-    kw = (dict(flashinfer64_valid_sequence=valid, cu_seqlens_q=cu.to(dev), cu_seqlens_kv=cu.to(dev)) if via == "valid"
-          else dict(cu_seqlens_q=cu, cu_seqlens_kv=cu))
+    if via == "valid":  # the host valid length alone (no cu_seqlens)
+        kw = dict(flashinfer64_valid_sequence=valid)
+    elif via == "device":  # device cu_seqlens only: the split stays on the device
+        kw = dict(cu_seqlens_q=cu.to(dev), cu_seqlens_kv=cu.to(dev))
+    else:
+        kw = dict(cu_seqlens_q=cu, cu_seqlens_kv=cu)
     out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=12, skip_steps=12, cache_interval=12,
                         layer_idx=0, sparsity=0.5, sparsity_dcrt=0.1, tile_size=16, video_len=vl,
                         video_perm=perm, max_seqlen_q=valid, max_seqlen_kv=valid, **kw)
@@ -225,30 +238,82 @@ def test_records_and_mask_export_from_a_call(dev, tmp_path):
         DFS_Attention.set_record_density(False)
 
 
-def test_overflow_check_reruns_on_bf16_operands(dev):
-    """V values beyond the f16 range: with DFS_Attention.check_overflow the
-    call is redone on bf16 operands and matches the fp32 oracle; the
-    default f16 path is documented to need inputs inside the f16 range."""
+def test_default_path_keeps_inputs_beyond_f16(dev):
+    """Default settings (f16 operands) with |v| and |q| far beyond the f16
+    range in some heads: every finite bf16 input is carried (per-head powers
+    of two, decided on the device), and the call matches the oracle's whole
+    call on the same inputs."""
     from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention
     from dfsattn_amd.utils.order import hilbert3d_perm
-    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
 
-    cfg = CONFIGS[0]
-    q, k, v = synth_qkv(cfg, dtype=torch.bfloat16)
-    v = v.clone()
-    v[:, :, 100, :] = 2.0e5  # bf16 holds it, f16 (max 65504) does not
+    cfg = DfsConfig("big", (4, 16, 16), 4, 128, torch.bfloat16, seed=5)
+    q, k, v = (x.clone() for x in synth_qkv(cfg))
+    v[:, 0] = (v[:, 0].float() * 2.0e5).to(torch.bfloat16)
+    q[:, 1] = (q[:, 1].float() * 1.0e5).to(torch.bfloat16)
+    v[:, 2, 100:140] = 7.0e4  # a few rows just past the f16 maximum
+    q[:, 3] = (q[:, 3].float() * 3.0e5).to(torch.bfloat16)
+    v[:, 3] = (v[:, 3].float() * 1.0e6).to(torch.bfloat16)
     perm = hilbert3d_perm(*cfg.grid)
-    DFS_Attention.check_overflow = True
-    try:
-        out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=24, skip_steps=12, cache_interval=12,
-                            layer_idx=5, sparsity=0.3, sparsity_dcrt=0.1, tile_size=16, video_perm=perm)
-    finally:
-        DFS_Attention.check_overflow = False
+    out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=24, skip_steps=12, cache_interval=12,
+                        layer_idx=5, sparsity=0.3, sparsity_dcrt=0.1, tile_size=16, video_perm=perm)
     assert bool(torch.isfinite(out).all())
     mask = DFS_Attention._cached_metadata[(5, "native", 128, 16, 16)]["block_mask"].cpu()
+    _, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.3, 16)
+    assert (mask == ref_mask).float().mean() > 0.97
     p, inv = orc.full_permutation(perm, q.shape[2])
     ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
-    assert _rel(out.cpu(), ref) < 6e-3  # bf16 operands and output
+    for h in range(4):
+        assert _rel(out.cpu()[:, h], ref[:, h]) < 4e-3, h  # bf16 output
+
+
+def test_wan_key_split_on_the_device(dev):
+    """Wan's cu_seqlens_q [0, S, S] with cu_seqlens_kv [0, s_k, S] (the
+    processor's form with an attention mask, replace_wan.py:246-250) as device
+    tensors: every query attends only the first s_k keys (execution order)
+    under the selected mask; no host read of the split."""
+    from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+
+    cfg = DfsConfig("wan-split", (3, 16, 20), 2, 128, torch.bfloat16, seed=8)
+    q, k, v = synth_qkv(cfg)
+    S, s_k = cfg.seq_len, 700
+    perm = hilbert3d_perm(*cfg.grid)
+    cq = torch.tensor([0, S, S], dtype=torch.int32, device=dev)
+    ck = torch.tensor([0, s_k, S], dtype=torch.int32, device=dev)
+    out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=24, skip_steps=12, cache_interval=12,
+                        layer_idx=9, sparsity=0.5, sparsity_dcrt=0.0, tile_size=16, video_perm=perm,
+                        cu_seqlens_q=cq, cu_seqlens_kv=ck, max_seqlen_q=S, max_seqlen_kv=S)
+    mask = DFS_Attention._cached_metadata[(9, "native", 128, 16, 16)]["block_mask"].cpu()
+    p, inv = orc.full_permutation(perm, S)
+    ref = orc.varlen_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask,
+                               [0, S, S], [0, s_k, S])[:, :, inv]
+    got = out.cpu().float()
+    assert _rel(got, ref) < 4e-3 and float((got - ref).abs().max()) < 2e-2
+    whole = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
+    assert _rel(got, whole) > 0.05  # the key split changes the result
+
+
+def test_dense_path_device_split_and_range(dev):
+    """full_attention("flash") with device cu_seqlens [0, valid, L] and V
+    beyond the f16 range: no host read of the split, the dense kernel keeps
+    every finite input, and both sequences match fp32 attention."""
+    from dfsattn_amd.fullattention import full_attention
+
+    torch.manual_seed(12)
+    L, valid = 700, 520
+    q, k, v = (torch.randn(1, 2, L, 128) for _ in range(3))
+    v[:, 1] *= 3.0e5
+    q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    cu = torch.tensor([0, valid, L], dtype=torch.int32, device=dev)
+    out = full_attention(q.to(dev), k.to(dev), v.to(dev), mode="flash", cu_seqlens_q=cu, cu_seqlens_kv=cu)
+    nb = math.ceil(L / 128)
+    ref = orc.segment_attention(q.float(), k.float(), v.float(), torch.ones(2, nb, nb, dtype=torch.bool),
+                                [0, valid, L])
+    assert bool(torch.isfinite(out).all())
+    for h in range(2):
+        assert _rel(out.cpu()[:, h], ref[:, h]) < 4e-3, h
 
 
 @pytest.mark.parametrize("grid,heads,d,dtype,sparsity", [

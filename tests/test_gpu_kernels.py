@@ -81,8 +81,7 @@ def test_prepare_qkv_matches_oracle(dev, case):
     vperm = torch.randperm(video)
     perm, _ = orc.full_permutation(vperm, length)
     layout = ScoringLayout(length, video, tile)
-    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout, operand_dtype=pv,
-                           check_overflow=True)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout, operand_dtype=pv)
     qp, kp, vp = (orc.apply_permutation(x, perm) for x in (q, k, v))
     R = layout.rows
     pad = lambda x: torch.cat([x[0], x.new_zeros(heads, R - length, d)], dim=1)
@@ -90,7 +89,8 @@ def test_prepare_qkv_matches_oracle(dev, case):
     assert torch.equal(prep.q_perm.cpu(), pad(qp).to(pv))
     assert torch.equal(prep.k_perm.cpu(), pad(kp).to(pv))
     assert torch.equal(prep.v_t.cpu(), vt_reference(pad(vp), pv))
-    assert int(prep.overflow.item()) == 0
+    if prep.exps is not None:  # bf16 inputs inside the f16 range: no head is rescaled
+        assert int(prep.exps.abs().sum().item()) == 0
     qt, kt = orc.pooled_tiles(qp, kp, tile, 128, video)
     for hi, lo, ref in ((prep.q_hi, prep.q_lo, qt[0]), (prep.k_hi, prep.k_lo, kt[0])):
         got = hi.cpu().float() + lo.cpu().float()
@@ -98,21 +98,65 @@ def test_prepare_qkv_matches_oracle(dev, case):
         assert torch.allclose(got, ref, rtol=2e-5, atol=1e-6), float((got - ref).abs().max())
 
 
-def test_prepare_flags_f16_overflow(dev):
-    """bf16 inputs rounded to f16 operands: a finite value beyond the f16 range
-    (in q, k or v) raises the overflow flag; bf16 operands keep the bits."""
-    heads, length, d = 1, 300, 64
+def test_prepare_rescales_heads_beyond_f16(dev):
+    """bf16 inputs rounded to f16 operands: a head holding a finite value
+    beyond the f16 range is stored as x * 2^-e, e the smallest exponent with
+    max|x| * 2^-e < 2^15 (1e6 = 2^19.93 -> e = 5), bit-exactly; every other
+    head keeps plain rounding and exponent 0. bf16 operands keep the bits and
+    carry no exponents."""
+    heads, length, d = 3, 300, 64
     layout = ScoringLayout(length, length, 16)
     ident = torch.arange(length, dtype=torch.int32, device=dev)
     for which in range(3):
         qkv = [torch.randn((1, heads, length, d)).to(torch.bfloat16) for _ in range(3)]
-        qkv[which][0, 0, 123, 7] = 1.0e6
-        prep = ops.prepare_qkv(*(x.to(dev) for x in qkv), ident, layout, check_overflow=True, pool=False)
-        assert int(prep.overflow.item()) == 1, which
-        keep = ops.prepare_qkv(*(x.to(dev) for x in qkv), ident, layout, operand_dtype=torch.bfloat16,
-                               check_overflow=True, pool=False)
-        assert int(keep.overflow.item()) == 0
+        qkv[which][0, 1, 123, 7] = 1.0e6
+        prep = ops.prepare_qkv(*(x.to(dev) for x in qkv), ident, layout, pool=False)
+        exps = prep.exps.cpu()
+        want = torch.zeros(3, heads, dtype=torch.int32)
+        want[which, 1] = 5
+        assert torch.equal(exps, want), (which, exps)
+        R = layout.rows
+        scaled = [x[0].float() for x in qkv]
+        scaled[which][1] *= 2.0 ** -5
+        for t, got in enumerate((prep.q_perm, prep.k_perm)):
+            ref = torch.cat([scaled[t].to(torch.float16), torch.zeros(heads, R - length, d, dtype=torch.float16)], 1)
+            assert torch.equal(got.cpu(), ref), (which, t)
+        pad = torch.cat([scaled[2], scaled[2].new_zeros(heads, R - length, d)], 1)
+        assert torch.equal(prep.v_t.cpu(), vt_reference(pad, torch.float16)), which
+        keep = ops.prepare_qkv(*(x.to(dev) for x in qkv), ident, layout, operand_dtype=torch.bfloat16, pool=False)
+        assert keep.exps is None
         assert torch.equal(keep.q_perm.cpu()[:, :length], qkv[0][0])
+
+
+@pytest.mark.parametrize("pv", (torch.float16, torch.bfloat16))
+def test_bsa_fwd_keeps_inputs_beyond_f16(dev, pv):
+    """Heads with q, k or v beyond the f16 range (q * scale * log2(e) beyond
+    it too, so rows carry their own power of two) against fp32 masked
+    attention of the same bf16 inputs."""
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+    heads, d, length = 4, 128, 1000
+    cfg = DfsConfig("big", (1, 1, length), heads, d, torch.bfloat16, seed=31)
+    q, k, v = (x.clone() for x in synth_qkv(cfg))
+    v[:, 0] = (v[:, 0].float() * 3.0e5).to(torch.bfloat16)        # V beyond f16
+    k[:, 1] = (k[:, 1].float() * 2.0e5).to(torch.bfloat16)        # K beyond f16
+    q[:, 2] = (q[:, 2].float() * 1.0e6).to(torch.bfloat16)        # Q, and Q * c, beyond f16
+    q[:, 3, :500] = (q[:, 3, :500].float() * 4.0e5).to(torch.bfloat16)  # only some rows of a head
+    k[:, 3] = (k[:, 3].float() * 1.0e2).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(32)
+    nb = math.ceil(length / 128)
+    mask = torch.rand((heads, nb, nb), generator=g) < 0.5
+    mask[:, torch.arange(nb), torch.arange(nb)] = True
+    layout = ScoringLayout(length, length, 16)
+    ident = torch.arange(length, dtype=torch.int32, device=dev)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident, layout, operand_dtype=pv, pool=False)
+    row_ptr, col_idx = ops.mask_to_csr(mask.to(dev))
+    got = ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=torch.float32).cpu()
+    ref = orc.masked_attention(q, k, v, mask)
+    assert bool(torch.isfinite(got).all())
+    for h in range(heads):
+        rel = mean_rel(got[:, h], ref[:, h])
+        print(f"head {h} ({pv}): mean-rel {rel:.2e}", flush=True)
+        assert rel <= (1e-3 if pv == torch.float16 else 3e-3), h
 
 
 def _random_scores(heads, rows, cols, seed, ties=False):
@@ -281,39 +325,29 @@ def test_block_scores_with_far_apart_logits(dev, direction, tile, one_pass):
     assert torch.allclose(got, ref, rtol=2e-3, atol=2e-5), float((got - ref).abs().max())
 
 
-def _run_bsa(dev, q, k, v, mask_bool, pv, out_dtype, perm=None):
+def _run_bsa(dev, q, k, v, mask_bool, pv, out_dtype, perm=None, scale=None):
     heads, length, d = q.shape[1], q.shape[2], q.shape[3]
     layout = ScoringLayout(length, length, 16)
     ident = torch.arange(length, dtype=torch.int32)
     prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident.to(dev), layout, operand_dtype=pv, pool=False)
     row_ptr, col_idx = ops.mask_to_csr(mask_bool.to(dev))
-    out = ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=out_dtype,
+    out = ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=out_dtype, scale=scale,
                       out_perm=None if perm is None else perm.to(dev, torch.int32))
     return out.cpu()
 
 
-SCHEDULES = ("pp", "split", "split+pair", "split+rotate")
+SCALES = (None, 0.6)  # the softmax scale: default D^-1/2, and one that sends every head to the scaled instance
 
 
-def _set_schedule(monkeypatch, schedule):
-    """DFSATTN_AMD_BSA_KERNEL (and DFSATTN_AMD_BSA_ORDER of the split schedule)."""
-    kernel, _, order = schedule.partition("+")
-    monkeypatch.setenv("DFSATTN_AMD_BSA_KERNEL", kernel)
-    if order:
-        monkeypatch.setenv("DFSATTN_AMD_BSA_ORDER", order)
-    else:
-        monkeypatch.delenv("DFSATTN_AMD_BSA_ORDER", raising=False)
-
-
-@pytest.mark.parametrize("schedule", SCHEDULES)
+@pytest.mark.parametrize("scale", SCALES)
 @pytest.mark.parametrize("d,length,density,pv", [
     (128, 1000, 0.3, torch.float16), (128, 1024, 0.5, torch.float16), (64, 1000, 0.3, torch.float16),
     (128, 3000, 0.3, torch.float16), (128, 1000, 1.0, torch.float16), (128, 1000, 0.3, torch.bfloat16),
     (64, 130, 1.0, torch.float16), (128, 1100, 0.3, torch.float16), (64, 1400, 0.2, torch.bfloat16)])
-def test_bsa_fwd_matches_masked_dense(dev, monkeypatch, schedule, d, length, density, pv):
-    """Every attention schedule (DFSATTN_AMD_BSA_KERNEL) against fp32 masked
-    attention; odd block counts leave the last query-block pair half empty."""
-    _set_schedule(monkeypatch, schedule)
+def test_bsa_fwd_matches_masked_dense(dev, scale, d, length, density, pv):
+    """The attention kernel against fp32 masked attention, at the default
+    softmax scale and at one large enough that every head runs in the scaled
+    instance (rows carrying their own powers of two)."""
     from dfsattn_amd.workloads import DfsConfig, synth_qkv
     heads = 2
     cfg = DfsConfig("t", (1, 1, length), heads, d, torch.bfloat16, seed=11)
@@ -322,14 +356,14 @@ def test_bsa_fwd_matches_masked_dense(dev, monkeypatch, schedule, d, length, den
     g = torch.Generator().manual_seed(12)
     mask = torch.rand((heads, nb, nb), generator=g) < density
     mask[:, torch.arange(nb), torch.arange(nb)] = True  # no empty rows
-    out = _run_bsa(dev, q, k, v, mask, pv, torch.float32)
-    ref = orc.masked_attention(q, k, v, mask)
+    out = _run_bsa(dev, q, k, v, mask, pv, torch.float32, scale=scale)
+    ref = orc.masked_attention(q, k, v, mask, scale=scale)
     max_abs = float((out - ref).abs().max())
     mr = mean_rel(out, ref)
     tol = 1e-3 if pv == torch.float16 else 3e-3  # bf16 P: reference-kernel precision class
     assert max_abs <= 2e-2 and mr <= tol, (max_abs, mr)
     if density == 1.0:
-        dense = orc.dense_attention(q, k, v)
+        dense = orc.dense_attention(q, k, v, scale=scale)
         assert mean_rel(out, dense) <= tol
 
 
@@ -349,24 +383,22 @@ def test_bsa_fwd_bf16_out_and_fused_unpermute(dev):
     assert torch.equal(scat[:, :, perm], out32)
 
 
-@pytest.mark.parametrize("schedule", SCHEDULES)
-def test_empty_rows_give_zero(dev, monkeypatch, schedule):
-    _set_schedule(monkeypatch, schedule)
+@pytest.mark.parametrize("scale", SCALES)
+def test_empty_rows_give_zero(dev, scale):
     heads, d, length = 1, 128, 512
     q, k, v = (torch.randn((1, heads, length, d)).to(torch.bfloat16) for _ in range(3))
     mask = torch.zeros((heads, 4, 4), dtype=torch.bool)
     mask[0, 0, 1] = True
-    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32)
+    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32, scale=scale)
     assert torch.count_nonzero(out[:, :, 128:]) == 0
-    ref = orc.masked_attention(q, k, v, mask)
+    ref = orc.masked_attention(q, k, v, mask, scale=scale)
     assert mean_rel(out[:, :, :128], ref[:, :, :128]) < 1e-3
 
 
-@pytest.mark.parametrize("schedule", SCHEDULES)
-def test_rows_keeping_only_a_short_tail_block(dev, monkeypatch, schedule):
+@pytest.mark.parametrize("scale", SCALES)
+def test_rows_keeping_only_a_short_tail_block(dev, scale):
     """The last block holds 26 keys: a wave whose keys of that block are all
     masked, and which has seen no other key, must contribute nothing."""
-    _set_schedule(monkeypatch, schedule)
     heads, d, length = 2, 128, 1050
     q, k, v = (torch.randn((1, heads, length, d), generator=torch.Generator().manual_seed(s)).to(torch.bfloat16)
                for s in (21, 22, 23))
@@ -379,19 +411,18 @@ def test_rows_keeping_only_a_short_tail_block(dev, monkeypatch, schedule):
     mask[:, 1, nb - 1] = True
     mask[:, nb - 1] = False
     mask[:, nb - 1, nb - 1] = True
-    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32)
+    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32, scale=scale)
     assert torch.isfinite(out).all()
-    ref = orc.masked_attention(q, k, v, mask)
+    ref = orc.masked_attention(q, k, v, mask, scale=scale)
     assert float((out - ref).abs().max()) <= 2e-2 and mean_rel(out, ref) <= 1e-3
 
 
-@pytest.mark.parametrize("schedule", SCHEDULES)
-def test_bsa_fwd_rising_and_negative_logits(dev, monkeypatch, schedule):
+@pytest.mark.parametrize("scale", SCALES)
+def test_bsa_fwd_rising_and_negative_logits(dev, scale):
     """Logits that grow block after block (the running maximum jumps by far
     more than the lazy-rescale threshold several times) and rows whose
     logits are all strongly negative: the output still equals fp32 masked
     attention."""
-    _set_schedule(monkeypatch, schedule)
     heads, d, length = 2, 128, 1200
     g = torch.Generator().manual_seed(21)
     q = torch.randn((1, heads, length, d), generator=g)
@@ -405,8 +436,8 @@ def test_bsa_fwd_rising_and_negative_logits(dev, monkeypatch, schedule):
     q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
     mask = torch.rand((heads, nb, nb), generator=g) < 0.6
     mask[:, torch.arange(nb), torch.arange(nb)] = True
-    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32)
-    ref = orc.masked_attention(q, k, v, mask)
+    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32, scale=scale)
+    ref = orc.masked_attention(q, k, v, mask, scale=scale)
     assert torch.isfinite(out).all()
     assert float((out - ref).abs().max()) <= 2e-2 and mean_rel(out, ref) <= 1e-3, \
         (float((out - ref).abs().max()), mean_rel(out, ref))
@@ -446,19 +477,27 @@ def test_wrappers_reject_bad_index_operands(dev):
     assert bool(torch.isfinite(out.float()).all())
 
 
-@pytest.mark.parametrize("schedule", ("pp", "split"))
-@pytest.mark.parametrize("length,valid", [(1300, 1100), (1300, 1152), (1000, 130), (1000, 1)])
-def test_bsa_fwd_valid_len_is_the_leading_sequence(dev, monkeypatch, schedule, length, valid):
-    """valid_len restricts a call to the first rows and keys: the result
-    equals masked attention of the leading sequence under the mask's leading
-    blocks (columns past them, kept in the CSR rows, are skipped), and rows
-    from valid_len on are left as they were."""
-    _set_schedule(monkeypatch, schedule)
+@pytest.mark.parametrize("length,cu_q,cu_k", [
+    (1300, [0, 1100, 1300], [0, 1100, 1300]),   # text padding: two sequences, blocks from each start
+    (1300, [0, 1152, 1300], [0, 1152, 1300]),   # a split on a block boundary
+    (1000, [0, 130, 1000], [0, 130, 1000]),     # a long second sequence
+    (1000, [0, 1, 1000], [0, 1, 1000]),         # a one-token first sequence
+    (1000, [0, 1000, 1000], [0, 700, 1000]),    # Wan's [0, S, S] / [0, s_k, S]: keys past s_k unused
+    (1000, [0, 600, 900], [0, 500, 1000]),      # unequal splits; rows 900.. in no sequence
+    (1000, [0, 1000], [0, 1000]),               # one sequence given explicitly
+    (900, [0, 0, 900], [0, 0, 900]),            # an empty first sequence
+])
+def test_bsa_fwd_varlen_matches_oracle(dev, length, cu_q, cu_k):
+    """Device cu_seqlens (block_sparse_attn_func's varlen arguments): sequence
+    i's queries attend its keys under the mask indexed from each sequence's
+    start; rows in no query sequence are zero; the offsets are never read on
+    the host. Against the fp32 varlen oracle, which tests pin to dense
+    attention under explicit token masks."""
     from dfsattn_amd.workloads import DfsConfig, synth_qkv
     heads, d = 2, 128
     cfg = DfsConfig("t", (1, 1, length), heads, d, torch.bfloat16, seed=21)
     q, k, v = synth_qkv(cfg)
-    nb, vb = math.ceil(length / 128), math.ceil(valid / 128)
+    nb = math.ceil(length / 128)
     g = torch.Generator().manual_seed(22)
     mask = torch.rand((heads, nb, nb), generator=g) < 0.4
     mask[:, torch.arange(nb), torch.arange(nb)] = True
@@ -467,9 +506,17 @@ def test_bsa_fwd_valid_len_is_the_leading_sequence(dev, monkeypatch, schedule, l
     prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident.to(dev), layout, pool=False)
     row_ptr, col_idx = ops.mask_to_csr(mask.to(dev))
     out = torch.full((1, heads, length, d), 7.0, dtype=torch.float32, device=dev)
-    ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=torch.float32, out=out, valid_len=valid)
-    out = out.cpu()
-    ref = orc.masked_attention(q[:, :, :valid], k[:, :, :valid], v[:, :, :valid], mask[:, :vb, :vb])
-    got = out[:, :, :valid]
+    cq = torch.tensor(cu_q, dtype=torch.int32, device=dev)
+    ck = torch.tensor(cu_k, dtype=torch.int32, device=dev)
+    _, lse = ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=torch.float32, out=out, cu_seqlens_q=cq,
+                         cu_seqlens_k=ck, want_lse=True)
+    got = out.cpu()
+    ref = orc.varlen_attention(q, k, v, mask, cu_q, cu_k)
     assert float((got - ref).abs().max()) <= 2e-2 and mean_rel(got, ref) <= 1e-3
-    assert bool((out[:, :, valid:] == 7.0).all())
+    covered = torch.zeros(length, dtype=torch.bool)
+    for (q0, q1), (k0, k1) in zip(zip(cu_q, cu_q[1:]), zip(cu_k, cu_k[1:])):
+        if k1 > k0:
+            covered[q0:q1] = True
+    assert bool((got[:, :, ~covered] == 0).all())
+    assert bool(torch.isneginf(lse.cpu()[:, ~covered]).all())
+    assert bool(torch.isfinite(lse.cpu()[:, covered]).all())

@@ -43,10 +43,18 @@ def test_abi_rejects_bad_arguments_without_launching():
         _lib.call("dfs_topk_from_scores", fake, 2, 8, 8, 8, 8, 9, 8, 8, fake, fake, None, None)
     with pytest.raises(_lib.DfsKernelError, match="f16 inputs"):
         _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 0, 0.1, fake, 2,
-                  None, None, 0, None)
-    with pytest.raises(_lib.DfsKernelError, match="valid_len"):
+                  None, None, None, None, 1, None, None)
+    with pytest.raises(_lib.DfsKernelError, match="n_seq=3"):
         _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 1, 0.1, fake, 2,
-                  None, None, 1001, None)
+                  None, None, fake, fake, 3, None, None)
+    with pytest.raises(_lib.DfsKernelError, match="both cu_seqlens_q and cu_seqlens_k"):
+        _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 1, 0.1, fake, 2,
+                  None, None, fake, None, 2, None, None)
+    with pytest.raises(_lib.DfsKernelError, match="two sequences need cu_seqlens"):
+        _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 1, 0.1, fake, 2,
+                  None, None, None, None, 2, None, None)
+    with pytest.raises(_lib.DfsKernelError, match="head_dim=96"):
+        _lib.call("dfs_prepare_fixup", fake, fake, fake, fake, 2, 1000, 96, fake, fake, fake, fake, fake, None)
     with pytest.raises(_lib.DfsKernelError, match="row_bytes"):
         _lib.call("dfs_permute_gather", fake, fake, fake, 1, 10, 10, 10, 3, None)
     with pytest.raises(_lib.DfsKernelError, match="positive"):
@@ -113,17 +121,19 @@ def test_flop_counts_use_valid_token_blocks():
 
 
 def test_cu_seqlens_forms():
-    """[0, L], [0, L, L] and [0, valid, L] give the valid length; other
-    splits are refused; device tensors are not read back."""
+    """Host cu_seqlens: [0, L] and [0, L, L] are one sequence, [0, a, L] a
+    split (including a = 0); other forms are refused. Device tensors are
+    never read back (their checks run on the GPU tests)."""
     from dfsattn_amd.core import DfsCore
-    check = DfsCore._check_cu_seqlens
-    assert check(None, 300) is None
-    assert check(torch.tensor([0, 300], dtype=torch.int32), 300) == 300
-    assert check(torch.tensor([0, 300, 300], dtype=torch.int32), 300) == 300
-    assert check(torch.tensor([0, 250, 300], dtype=torch.int32), 300) == 250
-    for bad in ([0, 100, 200, 300], [1, 300], [0, 310, 300], [0, 200]):
+    check = DfsCore._host_split
+    assert DfsCore._sequences(None, 300, torch.device("cpu"), "cu") is None
+    assert check([0, 300], 300) is None
+    assert check([0, 300, 300], 300) is None
+    assert check([0, 250, 300], 300) == [0, 250, 300]
+    assert check([0, 0, 300], 300) == [0, 0, 300]
+    for bad in ([0, 100, 200, 300], [1, 300], [0, 310, 300], [0, 200], [0, 200, 100, 300]):
         with pytest.raises(NotImplementedError):
-            check(torch.tensor(bad, dtype=torch.int32), 300)
+            check(bad, 300)
 
 
 @pytest.mark.parametrize("grid", [(1, 4, 4), (3, 5, 7), (2, 8, 8), (5, 3, 9), (1, 1, 1), (4, 16, 16), (2, 45, 80)])

@@ -162,6 +162,36 @@ def test_segment_attention_matches_block_diagonal_closed_form():
     assert torch.allclose(orc.segment_attention(q, k, v, mask, [0, 430, 430]), orc.masked_attention(q, k, v, mask))
 
 
+def test_varlen_attention_closed_forms():
+    """Separate query and key splits: sequence i's queries attend its own
+    keys, blocks counted from each side's start. Checked against dense
+    attention under the explicit token mask (a rectangular block-diagonal
+    layout), against segment_attention for equal splits, and rows outside
+    every query sequence stay zero."""
+    torch.manual_seed(6)
+    q, k, v = (torch.randn(1, 2, 430, 16) for _ in range(3))
+    mask = torch.rand(2, 4, 4) < 0.5
+    mask[:, :, 0] = True
+    assert torch.allclose(orc.varlen_attention(q, k, v, mask, [0, 300, 430], [0, 300, 430]),
+                          orc.segment_attention(q, k, v, mask, [0, 300, 430]))
+    # Wan's cross form: every query, keys [0, 250) only (an empty second sequence)
+    got = orc.varlen_attention(q, k, v, mask, [0, 430, 430], [0, 250, 430])
+    tok = torch.zeros(2, 430, 430, dtype=torch.bool)
+    tok[:, :, :250] = orc.expand_block_mask(mask, 430)[:, :, :250]
+    assert torch.allclose(got, orc.dense_attention(q, k, v, tok), atol=1e-5)
+    # unequal splits: queries [0, 200) / [200, 330) against keys [0, 260) / [260, 430)
+    got = orc.varlen_attention(q, k, v, mask, [0, 200, 330], [0, 260, 430])
+    tok = torch.zeros(2, 430, 430, dtype=torch.bool)
+    tok[:, :200, :260] = orc.expand_block_mask(mask, 260)[:, :200, :260]
+    tok[:, 200:330, 260:430] = orc.expand_block_mask(mask, 170)[:, :130, :170]
+    ref = orc.dense_attention(q, k, v, tok)
+    ref[:, :, 330:] = 0  # rows 330.. belong to no query sequence
+    assert torch.allclose(got, ref, atol=1e-5)
+    # a sequence without keys gives zero rows
+    got = orc.varlen_attention(q, k, v, mask, [0, 300, 430], [0, 430, 430])
+    assert torch.equal(got[:, :, 300:], torch.zeros_like(got[:, :, 300:]))
+
+
 def test_full_reference_call_is_permutation_consistent():
     torch.manual_seed(4)
     q, k, v = (torch.randn(1, 2, 256, 16) for _ in range(3))
