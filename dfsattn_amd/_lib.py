@@ -28,6 +28,8 @@ SIGNATURES = {
     "dfs_block_score_topk_workspace_size": [_i64, _i64, _i64, _i64],
     "dfs_block_score_topk": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p],
+    "dfs_block_score_topk_noalloc": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                     _i64, _i64, _i64, _p, _p, _p, _p],
     "dfs_topk_from_scores": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p],
     "dfs_prepare_fixup": [_p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p],
     "dfs_bsa_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _p, _i32, _p, _p, _p, _p, _i64, _p, _p],

@@ -16,6 +16,8 @@
 // row, emitting CSR column indices for the attention kernel.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "lds_copy.h"
 
@@ -631,29 +633,47 @@ int check_policy(const char* name, int64_t heads, int64_t q_blocks, int64_t k_bl
   return 0;
 }
 
-}  // namespace
-}  // namespace dfs
 
-extern "C" {
+// Scratch of the allocation-free entry point: the block-sum matrix of one
+// call, in a file-scope device array (one copy per GPU, held until the
+// process ends). In host code `scratch` names a host-side stand-in, so its
+// device address is looked up once per device and only that address is used.
+constexpr int64_t kScratchBytes = int64_t(96) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
-int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t tile_size, int64_t q_blocks,
-                                            int64_t k_blocks) {
-  if (heads <= 0 || q_blocks <= 0 || k_blocks <= 0 || (tile_size != 16 && tile_size != 32)) return -1;
-  const int64_t tpb = dfs::kBlock / tile_size, Gw = 4 * (32 / tpb);
-  const int64_t rows = (q_blocks + Gw - 1) / Gw * Gw * tpb;        // tile rows of every workgroup
-  const int64_t cols = (k_blocks * tpb + 31) / 32 * (32 / tpb);  // key blocks of every 32-tile chunk
-  return heads * rows * cols * static_cast<int64_t>(sizeof(float));
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch[kMaxDevices] = {};
+
+// The current device's scratch address (hipGetSymbolAddress on the first call
+// on that device, with that device current).
+int scratch_for_current_device(const char* name, float** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: no usable current device (%s)", name, hipGetErrorString(e));
+    return 2;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || !ptr) {
+      set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev, hipGetErrorString(rc));
+      return 2;
+    }
+    g_scratch[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return 0;
 }
 
-int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
-                         const uint16_t* k_pool_hi, const uint16_t* k_pool_lo, int64_t heads,
-                         int64_t head_dim, int64_t tile_size, int64_t q_blocks, int64_t k_blocks,
-                         int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
-                         int64_t dense_row, const int32_t* row_ptr, int32_t* col_idx,
-                         float* scores_out, uint8_t* mask_out, void* workspace, int64_t workspace_bytes,
-                         dfs_stream_t stream) {
-  using namespace dfs;
-  const char* name = "dfs_block_score_topk";
+int score_topk_impl(const char* name, const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
+                    const uint16_t* k_pool_hi, const uint16_t* k_pool_lo, int64_t heads, int64_t head_dim,
+                    int64_t tile_size, int64_t q_blocks, int64_t k_blocks, int64_t scored_rows, int64_t n_cand,
+                    int64_t k_pick, int64_t dense_col, int64_t dense_row, const int32_t* row_ptr,
+                    int32_t* col_idx, float* scores_out, uint8_t* mask_out, void* workspace,
+                    int64_t workspace_bytes, dfs_stream_t stream) {
   DFS_REQUIRE(q_pool_hi && q_pool_lo && k_pool_hi && k_pool_lo && row_ptr && col_idx,
               "%s: NULL operand", name);
   DFS_REQUIRE(head_dim == 64 || head_dim == 128, "%s: head_dim=%lld (supported: 64, 128)", name,
@@ -745,6 +765,56 @@ int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
   else
     score_topk_kernel<64, 4><<<grid, 256, smem, s>>>(p);
   return check_launch(name);
+}
+
+}  // namespace
+}  // namespace dfs
+
+extern "C" {
+
+int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t tile_size, int64_t q_blocks,
+                                            int64_t k_blocks) {
+  if (heads <= 0 || q_blocks <= 0 || k_blocks <= 0 || (tile_size != 16 && tile_size != 32)) return -1;
+  const int64_t tpb = dfs::kBlock / tile_size, Gw = 4 * (32 / tpb);
+  const int64_t rows = (q_blocks + Gw - 1) / Gw * Gw * tpb;        // tile rows of every workgroup
+  const int64_t cols = (k_blocks * tpb + 31) / 32 * (32 / tpb);  // key blocks of every 32-tile chunk
+  return heads * rows * cols * static_cast<int64_t>(sizeof(float));
+}
+
+int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
+                         const uint16_t* k_pool_hi, const uint16_t* k_pool_lo, int64_t heads,
+                         int64_t head_dim, int64_t tile_size, int64_t q_blocks, int64_t k_blocks,
+                         int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
+                         int64_t dense_row, const int32_t* row_ptr, int32_t* col_idx,
+                         float* scores_out, uint8_t* mask_out, void* workspace, int64_t workspace_bytes,
+                         dfs_stream_t stream) {
+  return dfs::score_topk_impl("dfs_block_score_topk", q_pool_hi, q_pool_lo, k_pool_hi, k_pool_lo, heads, head_dim,
+                              tile_size, q_blocks, k_blocks, scored_rows, n_cand, k_pick, dense_col, dense_row,
+                              row_ptr, col_idx, scores_out, mask_out, workspace, workspace_bytes, stream);
+}
+
+int dfs_block_score_topk_noalloc(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
+                                 const uint16_t* k_pool_hi, const uint16_t* k_pool_lo, int64_t heads,
+                                 int64_t head_dim, int64_t tile_size, int64_t q_blocks, int64_t k_blocks,
+                                 int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
+                                 int64_t dense_row, const int32_t* row_ptr, int32_t* col_idx,
+                                 uint8_t* mask_out, dfs_stream_t stream) {
+  using namespace dfs;
+  const char* name = "dfs_block_score_topk_noalloc";
+  DFS_REQUIRE(heads > 0 && scored_rows > 0 && k_blocks > 0, "%s: empty problem", name);
+  const int64_t need = heads * scored_rows * k_blocks * static_cast<int64_t>(sizeof(float));
+  DFS_REQUIRE(need <= kScratchBytes,
+              "%s: the block sums of %lld heads x %lld rows x %lld key blocks need %lld bytes; the "
+              "library's scratch holds %lld (use dfs_block_score_topk with caller buffers)",
+              name, (long long)heads, (long long)scored_rows, (long long)k_blocks, (long long)need,
+              (long long)kScratchBytes);
+  float* sums = nullptr;
+  if (int rc = scratch_for_current_device(name, &sums)) return rc;
+  // Two-pass form: the block sums are the only scratch (every entry is
+  // written by the kernel, so nothing needs clearing between calls).
+  return score_topk_impl(name, q_pool_hi, q_pool_lo, k_pool_hi, k_pool_lo, heads, head_dim, tile_size, q_blocks,
+                         k_blocks, scored_rows, n_cand, k_pick, dense_col, dense_row, row_ptr, col_idx, sums,
+                         mask_out, nullptr, 0, stream);
 }
 
 int dfs_topk_from_scores(const float* scores, int64_t heads, int64_t q_blocks, int64_t k_blocks,

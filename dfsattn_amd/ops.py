@@ -220,6 +220,28 @@ def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
     return col_idx, (scores if want_scores else None), mask
 
 
+def block_score_topk_noalloc(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
+                             want_mask: bool = False):
+    """block_score_topk through the allocation-free entry point: the block
+    sums live in the library's static per-GPU scratch (at most 96 MiB), so
+    the kernels allocate nothing; only col_idx (and the optional mask) are
+    the caller's. Returns (col_idx, mask or None)."""
+    if prep.q_hi is None:
+        raise ValueError("prepare_qkv was called without pooling")
+    _require_device(prep.q_hi, row_ptr)
+    _require_int32(row_ptr=row_ptr)
+    if row_ptr.numel() != prep.heads * policy.q_blocks + 1:
+        raise ValueError(f"row_ptr has {row_ptr.numel()} entries for {prep.heads} x {policy.q_blocks} rows")
+    dev = prep.q_perm.device
+    col_idx = torch.empty(policy.nnz(prep.heads), dtype=torch.int32, device=dev)
+    mask = (torch.empty((prep.heads, policy.q_blocks, policy.k_blocks), dtype=torch.uint8, device=dev)
+            if want_mask else None)
+    _lib.call("dfs_block_score_topk_noalloc", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi), _ptr(prep.k_lo),
+              prep.heads, prep.head_dim, prep.layout.tile, *_policy_args(policy), _ptr(row_ptr), _ptr(col_idx),
+              _ptr(mask), _stream(prep.q_perm))
+    return col_idx, mask
+
+
 def topk_from_scores(scores: torch.Tensor, policy: TopkPolicy, row_ptr: torch.Tensor,
                      want_mask: bool = False):
     """Top-k of given fp32 block scores [H, scored_rows, Kb] under ``policy``;

@@ -167,6 +167,28 @@ int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t tile_size,
                                             int64_t q_blocks, int64_t k_blocks);
 
 /*
+ * dfs_block_score_topk that allocates nothing and takes no caller scratch:
+ * the block-sum matrix (heads * scored_rows * k_blocks fp32 values, at most
+ * 96 MiB: 55.9 MB at 75.6k tokens x 40 heads, 83.0 MB at 119k tokens x 24
+ * heads) lives in a static device array of the library, one per GPU, held
+ * until the process ends; larger problems are rejected with an error. Runs
+ * the two-pass form (no workspace); same selection as dfs_block_score_topk
+ * with scores_out and no workspace. Calls that overlap on one GPU (several
+ * streams or threads) share that array and race; serialise them. No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+int dfs_block_score_topk_noalloc(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
+                                 const uint16_t* k_pool_hi, const uint16_t* k_pool_lo,
+                                 int64_t heads, int64_t head_dim, int64_t tile_size,
+                                 int64_t q_blocks, int64_t k_blocks,
+                                 int64_t scored_rows, int64_t n_cand, int64_t k_pick,
+                                 int64_t dense_col, int64_t dense_row,
+                                 const int32_t* row_ptr, int32_t* col_idx,
+                                 uint8_t* mask_out, dfs_stream_t stream);
+
+/*
  * Top-k from given fp32 block scores [H][scored_rows][Kb] with the policy
  * above; emits CSR columns and an optional uint8 mask. Given the same fp32
  * scores it selects exactly the set torch.topk + scatter_ selects when no tie

@@ -55,6 +55,11 @@ def test_abi_rejects_bad_arguments_without_launching():
                   None, None, None, None, 2, None, None)
     with pytest.raises(_lib.DfsKernelError, match="head_dim=96"):
         _lib.call("dfs_prepare_fixup", fake, fake, fake, fake, 2, 1000, 96, fake, fake, fake, fake, fake, None)
+    # the allocation-free scorer refuses block sums beyond its 96 MiB scratch
+    # before touching a device (64 heads x 1000 x 1000 blocks = 256 MB)
+    with pytest.raises(_lib.DfsKernelError, match="scratch holds 100663296"):
+        _lib.call("dfs_block_score_topk_noalloc", fake, fake, fake, fake, 64, 128, 16, 1000, 1000, 1000, 1000, 300,
+                  1000, 1000, fake, fake, None, None)
     with pytest.raises(_lib.DfsKernelError, match="row_bytes"):
         _lib.call("dfs_permute_gather", fake, fake, fake, 1, 10, 10, 10, 3, None)
     with pytest.raises(_lib.DfsKernelError, match="positive"):
