@@ -1,0 +1,100 @@
+"""the mask-cache regime at the 75.6k-token Wan shape. 50
+sequential denoising calls with Q_t = Q_{t-1} + N(0, 0.02) (likewise K):
+the first 12 real steps dense, then dfs_attention with skip 12, interval 12
+and the step counter counting CFG passes (attention_wan.py:41-66, 432-470,
+792-800). Checks the refresh steps and their top-k sizes for sparsity 0.3
+with the reference's default decay 0.1 and without decay, that cached calls
+reuse the refreshed columns bit for bit, the fresh selection against the
+oracle's fp32 scores, and sampled query blocks of one refresh call and one
+cached call against fp32 masked attention (fp32 output, 1e-3 mean-rel)."""
+import pytest
+import torch
+
+from oracle import dfs_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(out, ref):
+    return float((out.double() - ref.double()).abs().mean() / ref.double().abs().mean())
+
+
+def _check_output(dev, entry, q, k, v, full, perm_d, lay, out_bf16, label):
+    """fp32 output of the call's operands and cached mask, on sampled query
+    blocks of two heads, against fp32 masked attention."""
+    from dfsattn_amd import ops
+    H, L = q.shape[1], q.shape[2]
+    heads = [0, H - 1]
+    qbs = [0, lay.q_blocks // 2, lay.q_blocks - 1]
+    mask = entry["block_mask"].cpu()
+    sub = [orc.apply_permutation(t[:, heads].float().cpu(), full) for t in (q, k, v)]
+    ref = orc.masked_attention(*sub, mask[heads], 128, q_blocks=qbs)
+    rows = torch.cat([torch.arange(b * 128, min((b + 1) * 128, L)) for b in qbs])
+    prep = ops.prepare_qkv(q, k, v, perm_d, lay, pool=False)
+    out32 = ops.bsa_fwd(prep, entry["row_ptr"], entry["col_idx"], out_dtype=torch.float32)
+    g32, r = out32[:, heads].cpu()[:, :, rows], ref[:, :, rows]
+    max_abs, mr = float((g32 - r).abs().max()), _rel(g32, r)
+    print(f"{label}: fp32 output max-abs {max_abs:.2e}, mean-rel {mr:.2e}", flush=True)
+    assert max_abs <= 2e-2 and mr <= 1e-3
+    # the call's own (bf16) output is the same computation, rounded
+    got = out_bf16[:, heads].cpu()[:, :, full][:, :, rows].float()
+    assert _rel(got, g32) < 4e-3
+
+
+@pytest.mark.parametrize("dcrt,expect", [(0.1, {12: 177, 24: 118, 36: 59}),
+                                         (0.0, {12: 177, 24: 177, 36: 177, 48: 177})])
+def test_mask_cache_regime_at_cfg1_shape(dev, dcrt, expect):
+    from dfsattn_amd import ops
+    from dfsattn_amd.attention_wan import DFS_Attention, _dfs_attention_instances, dfs_attention
+    from dfsattn_amd.fullattention import full_attention
+    from dfsattn_amd.layout import ScoringLayout
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[1]
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()
+    q, k, v = synth_qkv(cfg, device=dev)
+    perm = hilbert3d_perm(*cfg.grid)
+    L = cfg.seq_len
+    full, _ = orc.full_permutation(perm, L)
+    perm_d = ops.device_perm(full, dev)
+    lay = ScoringLayout(L, L, cfg.tile)
+    gen = torch.Generator(device=dev).manual_seed(33)
+    key = (0, "native", 128, 16, 16)
+    refreshes, kept_cols, prev = {}, None, None
+    for t in range(50):
+        if t > 0:  # the drift of the configuration: N(0, 0.02) per step on Q and K
+            q = (q.float() + 0.02 * torch.randn(q.shape, generator=gen, device=dev)).to(q.dtype)
+            k = (k.float() + 0.02 * torch.randn(k.shape, generator=gen, device=dev)).to(k.dtype)
+        if t < 12:  # dense warm-up steps (replace_wan.py:252-302)
+            if t in (0, 11):
+                dense = full_attention(q, k, v, mode="flash")
+                assert bool(torch.isfinite(dense).all())
+            continue
+        out = dfs_attention(q, k, v, step_idx=2 * t, skip_steps=12, cache_interval=12, layer_idx=0,
+                            sparsity=0.3, sparsity_dcrt=dcrt, tile_size=cfg.tile, video_perm=perm, cache_flag=True)
+        entry = DFS_Attention._cached_metadata[key]
+        if entry is not prev:  # a refresh stored a new entry
+            kpick = int((entry["row_ptr"][1] - entry["row_ptr"][0]).item())
+            refreshes[t] = kpick
+            kept_cols = entry["col_idx"].clone()
+            if t == 24:  # the fresh selection of head 0 against the oracle's fp32 scores
+                qp = orc.apply_permutation(q[:, :1].float().cpu(), full)
+                kp = orc.apply_permutation(k[:, :1].float().cpu(), full)
+                ref_scores = orc.block_scores(qp, kp, cfg.tile, 128, None, head_chunk=1)
+                ref_mask = orc.mask_from_scores_torch(ref_scores, kpick)
+                agree = float((entry["block_mask"][:1].cpu() == ref_mask).all(-1).float().mean())
+                print(f"dcrt {dcrt} step {t}: rows selected as from the oracle's scores: {agree:.4f}", flush=True)
+                assert agree >= 0.98
+            if t == 12:
+                _check_output(dev, entry, q, k, v, full, perm_d, lay, out, f"dcrt {dcrt} refresh step {t}")
+        else:
+            assert torch.equal(entry["col_idx"], kept_cols)  # the cached columns, bit for bit
+            if t == 13:
+                _check_output(dev, entry, q, k, v, full, perm_d, lay, out, f"dcrt {dcrt} cached step {t}")
+        prev = entry
+    print(f"dcrt {dcrt}: refreshes at real steps {refreshes}", flush=True)
+    assert refreshes == expect
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()

@@ -311,3 +311,68 @@ def test_dit_fused_elementwise_matches_torch_block(dev):
         dit.DiTBlock.fused_elementwise = True
     assert bool(torch.isfinite(fused).all())
     assert _rel(fused.cpu(), plain.cpu()) < 1e-2
+
+
+@torch.no_grad()
+def test_full_width_block_matches_fp32_reference(dev):
+    """One block at the cfg4 width (hidden 5,120, 40 heads of 128, FFN
+    13,824, QK-RMSNorm across heads, 3D RoPE, 512 x 4,096 text context) on
+    a reduced 3 x 16 x 20 token grid: a DFS refresh step (fresh masks, fused
+    norm/RoPE and block kernels, bf16) and a dense step against the same
+    weights in fp32 on the host, with the self-attention recomputed over the
+    masks the GPU selected (replace_wan.py:153-218, 252-302)."""
+    from dfsattn_amd import dit
+    from dfsattn_amd.attention_wan import DFS_Attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    cfg = dit.DiTConfig("cfg4-block", layers=1, grid=(3, 16, 20))
+    assert (cfg.dim, cfg.heads, cfg.head_dim, cfg.ffn_dim, cfg.text_len, cfg.text_dim) == (5120, 40, 128, 13824,
+                                                                                          512, 4096)
+    model = dit.build_model(cfg, dev)
+    latent, ctx, _ = dit.synth_inputs(cfg, dev)
+    t = torch.tensor([700.0], device=dev)
+    perm = hilbert3d_perm(*cfg.grid)
+    procs = dit.install_dfs_processors(model, "dfs", 0.3, 16, 128, perm, skip_steps=12, cache_interval=12)
+    captured = {}
+
+    def keep(name):
+        def hook(module, args, output):
+            captured[name] = output.float().cpu()
+        return hook
+
+    self_attn = model.attention_modules()[0][1]
+    handle = self_attn.register_forward_hook(keep("attn"))
+    dit.set_step(procs, 24)  # real step 12: mask refresh
+    sparse = model(latent, t, ctx).cpu()
+    sparse_attn = captured["attn"]
+    masks = {key[0]: e["block_mask"].cpu() for key, e in DFS_Attention._cached_metadata.items()}
+    assert sorted(masks) == [0]
+    dit.set_step(procs, 0)  # real step 0 < skip_steps: dense
+    dense = model(latent, t, ctx).cpu()
+    dense_attn = captured["attn"]
+    handle.remove()
+
+    ref_model = dit.WanLikeDiT(cfg, device="cpu", dtype=torch.float32).eval()
+    ref_model.load_state_dict({k: v.float().cpu() for k, v in model.state_dict().items()})
+    del model
+    full, inv = orc.full_permutation(perm, cfg.seq_len)
+    (n1, m1), (n2, m2) = ref_model.attention_modules()
+    m1.register_forward_hook(keep("ref_attn"))
+    m2.set_processor(_RefProcessor())
+    m1.set_processor(_RefProcessor(masks[0], full, inv))
+    ref_sparse = ref_model(latent.cpu(), t.cpu(), ctx.cpu())
+    ref_sparse_attn = captured["ref_attn"]
+    m1.set_processor(_RefProcessor())
+    ref_dense = ref_model(latent.cpu(), t.cpu(), ctx.cpu())
+    ref_dense_attn = captured["ref_attn"]
+    for got, ref, label in ((sparse, ref_sparse, "DFS refresh step"), (dense, ref_dense, "dense step"),
+                            (sparse_attn, ref_sparse_attn, "DFS self-attention output"),
+                            (dense_attn, ref_dense_attn, "dense self-attention output")):
+        assert bool(torch.isfinite(got).all())
+        rel = _rel(got, ref)
+        print(f"full-width block, {label} vs fp32 host reference: mean-rel {rel:.2e}", flush=True)
+        assert rel < 3e-2
+    # the masks matter at this width: sparse and dense self-attention differ
+    # by far more than either differs from its fp32 reference
+    gap = _rel(sparse_attn, dense_attn)
+    print(f"full-width block: sparse vs dense self-attention output, mean-rel {gap:.2e}", flush=True)
+    assert gap > 3 * _rel(sparse_attn, ref_sparse_attn)
