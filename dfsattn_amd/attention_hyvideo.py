@@ -19,6 +19,8 @@ import torch.nn as nn
 from .attention_wan import _compute_cache_schedule
 from .core import DfsCore, MaskEntry, block_interactions
 from .layout import ScoringLayout, TopkPolicy, hunyuan_policy
+from .utils import records
+from .utils.logger import logger
 from .utils.timing import AttentionTimingRecorder
 
 _dfs_attention_instances: Dict[int, "DFS_Attention"] = {}
@@ -111,6 +113,71 @@ class DFS_Attention(DfsCore, nn.Module):
     @classmethod
     def get_sparsity_records(cls):
         return cls.sparsity_records
+
+    @classmethod
+    def set_record_density(cls, enabled: bool):
+        super().set_record_density(enabled)
+        if not cls.record_density:
+            cls.sparsity_records.clear()
+
+    @classmethod
+    def dump_density_records(cls, output_path: Optional[str] = None) -> Optional[str]:
+        """Prints the density records as the reference's table and, with
+        ``output_path``, writes the density CSV with the route statistics
+        columns (attention_hyvideo.py:1511-1573 define the format)."""
+        if not cls.density_records:
+            logger.warning("No density records found. Make sure record_density was enabled during generation.")
+            return None
+        for line in records.density_report(cls.density_records):
+            print(line)
+        if output_path is not None:
+            records.write_density(output_path, cls.density_records, cls.sparsity_records)
+            print(f"Density records saved to: {output_path}")
+        return output_path
+
+    @classmethod
+    def dump_density_summary(cls, output_path: Optional[str] = None, prompt_idx: Optional[int] = None,
+                             prompt: Optional[str] = None) -> Optional[str]:
+        """Appends one prompt's density summary row to ``output_path``
+        (attention_hyvideo.py:1575-1691; the HunyuanVideo driver calls it
+        after generation, hyvideo_t2v_inference.py:390-396)."""
+        if not cls.density_records:
+            logger.warning("No density records found. Make sure record_density was enabled during generation.")
+            return None
+        row = records.density_summary(cls.density_records, cls.sparsity_records, prompt_idx, prompt)
+        if output_path is not None:
+            records.append_summary(output_path, row)
+            logger.info("Sparse density summary saved to %s", output_path)
+        return output_path
+
+    @classmethod
+    def dump_sparsity_records(cls, output_path: Optional[str] = None) -> Optional[str]:
+        """Per-(step, layer) sparsity statistics as CSV
+        (attention_hyvideo.py:1693-1727)."""
+        if not cls.sparsity_records:
+            logger.warning("No sparsity records found. Make sure --record_density true was enabled.")
+            return None
+        if output_path is not None:
+            records.write_sparsity(output_path, cls.sparsity_records)
+            logger.info("Sparsity records saved to %s", output_path)
+        return output_path
+
+    @classmethod
+    def configure_subblock_retention_profile(cls, output_dir: Optional[str], masses: Tuple[float, ...] = (0.9,)):
+        """The reference profiles fine-tile score mass inside selected blocks
+        here (attention_hyvideo.py:1315-1324, utils/subblock_retention.py).
+        The native scorer never materialises per-tile scores, so only
+        ``output_dir=None`` (profiling off, the driver's default,
+        hyvideo_t2v_inference.py:238) is accepted."""
+        if output_dir is not None:
+            raise NotImplementedError("sub-block retention profiling needs per-tile scores, which the native "
+                                      "scoring kernel does not write; call with output_dir=None")
+
+    @classmethod
+    def dump_subblock_retention_profile(cls) -> Optional[str]:
+        """Nothing is profiled (see configure_subblock_retention_profile): None,
+        as the reference returns with profiling off."""
+        return None
 
 
 def dfs_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, step_idx: int = 0, skip_steps: int = 12,

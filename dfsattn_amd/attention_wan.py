@@ -9,10 +9,8 @@ libdfsattn_amd.so; there is no CPU path.
 """
 from __future__ import annotations
 
-import csv
 import math
-import os
-from typing import Any, Dict, List, Optional, Tuple
+from typing import Any, Dict, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -20,6 +18,7 @@ import torch.nn as nn
 from . import ops
 from .core import DfsCore, MaskEntry, operand_dtype_for
 from .layout import ScoringLayout, TopkPolicy, wan_policy
+from .utils import records
 from .utils.logger import logger
 from .utils.timing import AttentionTimingRecorder
 
@@ -115,42 +114,16 @@ class DFS_Attention(DfsCore, nn.Module):
 
     @classmethod
     def dump_density_records(cls, output_path: Optional[str] = None) -> Optional[str]:
-        """Prints and saves the execution-tile records (attention_wan.py:604-661)."""
-        records = cls.execution_tile_records
-        if not records:
+        """Prints the execution-tile records as the reference's table and,
+        with ``output_path``, writes them as its CSV (attention_wan.py:604-661
+        define the format)."""
+        if not cls.execution_tile_records:
             logger.warning("No density records found. Make sure record_density was enabled during generation.")
             return None
-        flat: List[Dict[str, Any]] = []
-        for step in sorted(records):
-            for layer, metrics in sorted(records[step].items()):
-                flat.append({"step_idx": step, "layer_idx": layer, **metrics})
-        header = f"{'step_idx':>9} {'layer_idx':>10} {'backend':>10} {'tile':>6} {'k(mean)':>9} {'D_HW':>9}"
-        print("\n===== DFS Attention execution-tile records =====")
-        print(header)
-        print("-" * len(header))
-        step_sums: Dict[int, float] = {}
-        step_counts: Dict[int, int] = {}
-        for row in flat:
-            step = int(row["step_idx"])
-            density = float(row["execution_tile_density"])
-            step_sums[step] = step_sums.get(step, 0.0) + density
-            step_counts[step] = step_counts.get(step, 0) + 1
-            print(f"{step:>9} {int(row['layer_idx']):>10} {str(row['execution_backend']):>10} "
-                  f"{int(row['execution_tile_size']):>6} {float(row['tile_k_mean']):>9.2f} {density:>9.4f}")
-        all_mean = sum(float(r["execution_tile_density"]) for r in flat) / len(flat)
-        print(f"\nMean execution-tile density: {all_mean:.4f} ({all_mean * 100:.2f}%)")
-        step_mean = sum(step_sums[s] / step_counts[s] for s in step_sums) / len(step_sums)
-        print(f"Mean per-step execution-tile density: {step_mean:.4f} ({step_mean * 100:.2f}%)")
-        print("================================================")
+        for line in records.execution_tile_report(cls.execution_tile_records):
+            print(line)
         if output_path is not None:
-            os.makedirs(os.path.dirname(output_path) or ".", exist_ok=True)
-            fields = ["step_idx", "layer_idx", "execution_backend", "execution_tile_size", "q_tile_rows",
-                      "k_tile_cols", "tile_k_mean", "tile_k_min", "tile_k_max", "tiles_executed", "tiles_dense",
-                      "execution_tile_density"]
-            with open(output_path, "w", newline="") as fh:
-                writer = csv.DictWriter(fh, fieldnames=fields)
-                writer.writeheader()
-                writer.writerows(flat)
+            records.write_execution_tiles(output_path, cls.execution_tile_records)
             print(f"Execution-tile records saved to: {output_path}")
         return output_path
 

@@ -1,75 +1,62 @@
-"""Low-perturbation GPU timing of attention phases (dfsattn/utils/timing.py:24-218).
+"""Low-perturbation timing of attention phases, written out in the CSV form of
+dfsattn/utils/timing.py:97-218 (the same rows and columns).
 
-Events are recorded on the current stream without synchronising; durations
-are resolved when ``rows`` / ``dump_csv`` is called after the run.
+A measurement is a pair of marks taken around a phase. On a GPU device a mark
+is a HIP event recorded on the current stream, so taking it never waits for
+the device; on other devices it is a ``perf_counter`` reading. Marks are kept
+unresolved in one ledger per phase and turned into milliseconds together, with
+a single device synchronisation, the first time a summary is asked for after
+new GPU marks were added.
 """
 from __future__ import annotations
 
 import csv
 import os
 import time
-from dataclasses import dataclass
-from typing import Any, Dict, List, Optional, Union
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
+Mark = object  # a torch.cuda.Event or a perf_counter() float
 
-@dataclass
-class _EventPair:
-    phase: str
-    step_idx: int
-    layer_idx: int
-    start: Union[torch.cuda.Event, float]
-    end: Union[torch.cuda.Event, float]
+
+def _take_mark(device: torch.device) -> Mark:
+    if device.type == "cuda":
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        return ev
+    return time.perf_counter()
+
+
+def _span_ms(first: Mark, last: Mark) -> float:
+    if isinstance(first, torch.cuda.Event):
+        return float(first.elapsed_time(last))
+    return (float(last) - float(first)) * 1e3
+
+
+class _Ledger:
+    """The spans of one phase: unresolved mark pairs plus settled durations
+    (each with the step and layer it was recorded for)."""
+
+    __slots__ = ("open_pairs", "settled")
+
+    def __init__(self) -> None:
+        self.open_pairs: List[Tuple[Mark, Mark, int, int]] = []
+        self.settled: List[Tuple[float, int, int]] = []
+
+    def needs_device(self) -> bool:
+        return any(isinstance(a, torch.cuda.Event) for a, _, _, _ in self.open_pairs)
+
+    def settle(self) -> None:
+        self.settled.extend((_span_ms(a, b), s, l) for a, b, s, l in self.open_pairs)
+        self.open_pairs = []
+
+    def total_ms(self) -> float:
+        return sum(ms for ms, _, _ in self.settled)
 
 
 class AttentionTimingRecorder:
-    def __init__(self, enabled: bool = False) -> None:
-        self.enabled = enabled
-        self._records: List[_EventPair] = []
-        self._metric_records: Dict[str, List[float]] = {}
-
-    def reset(self, enabled: bool) -> None:
-        self.enabled = enabled
-        self._records.clear()
-        self._metric_records.clear()
-
-    def record_metrics(self, metrics: Dict[str, float]) -> None:
-        if not self.enabled:
-            return
-        for name, value in metrics.items():
-            self._metric_records.setdefault(name, []).append(float(value))
-
-    def start(self, device: torch.device):
-        if not self.enabled:
-            return None
-        if device.type == "cuda":
-            ev = torch.cuda.Event(enable_timing=True)
-            ev.record()
-            return ev
-        return time.perf_counter()
-
-    def stop(self, start, phase: str, step_idx: int, layer_idx: int, device: torch.device) -> None:
-        if not self.enabled or start is None:
-            return
-        if device.type == "cuda":
-            end = torch.cuda.Event(enable_timing=True)
-            end.record()
-        else:
-            end = time.perf_counter()
-        self._records.append(_EventPair(phase, int(step_idx), int(layer_idx), start, end))
-
-    def rows(self) -> List[Dict[str, Any]]:
-        if any(isinstance(r.end, torch.cuda.Event) for r in self._records):
-            torch.cuda.synchronize()
-        out = []
-        for r in self._records:
-            if isinstance(r.start, torch.cuda.Event):
-                ms = r.start.elapsed_time(r.end)
-            else:
-                ms = (r.end - r.start) * 1e3
-            out.append({"phase": r.phase, "step_idx": r.step_idx, "layer_idx": r.layer_idx, "elapsed_ms": ms})
-        return out
+    """Per-phase timing of DFS calls; disabled recorders take no marks."""
 
     # Phases of the reference's CSV besides the two this build records: its
     # research executors time these sub-phases (timing.py:113-138). They are
@@ -85,44 +72,90 @@ class AttentionTimingRecorder:
     )
     METRIC_FIELDS = ("residual_count_mean", "residual_count_p50", "residual_count_p95", "residual_count_max",
                      "residual_count_nonempty_ratio", "fine_top_k", "occupancy_threshold", "occupancy_mean")
+    # Recorded phase name -> CSV row it is summed into.
+    _CSV_ROW = {"topk_mask": "top_k_selection", "attention_execution": "attention_execution"}
+
+    def __init__(self, enabled: bool = False) -> None:
+        self.enabled = enabled
+        self._ledgers: Dict[str, _Ledger] = {}
+        self._metric_snapshots: List[Dict[str, float]] = []
+
+    def reset(self, enabled: bool) -> None:
+        """Drop everything recorded and switch recording on or off."""
+        self.enabled = enabled
+        self._ledgers = {}
+        self._metric_snapshots = []
+
+    def record_metrics(self, metrics: Dict[str, float]) -> None:
+        """One snapshot of route statistics; the CSV reports each field's
+        mean over the snapshots that carry it."""
+        if self.enabled:
+            self._metric_snapshots.append({k: float(v) for k, v in metrics.items()})
+
+    def start(self, device: torch.device) -> Optional[Mark]:
+        """Opening mark of a phase (None when disabled)."""
+        return _take_mark(device) if self.enabled else None
+
+    def stop(self, start: Optional[Mark], phase: str, step_idx: int, layer_idx: int, device: torch.device) -> None:
+        """Closes the span opened by ``start`` and files it under ``phase``."""
+        if not self.enabled or start is None:
+            return
+        ledger = self._ledgers.setdefault(phase, _Ledger())
+        ledger.open_pairs.append((start, _take_mark(device), int(step_idx), int(layer_idx)))
+
+    def _settle(self) -> None:
+        if any(ledger.needs_device() for ledger in self._ledgers.values()):
+            torch.cuda.synchronize()
+        for ledger in self._ledgers.values():
+            ledger.settle()
+
+    def rows(self) -> List[Dict[str, object]]:
+        """Every settled span as {phase, step_idx, layer_idx, elapsed_ms}."""
+        self._settle()
+        return [{"phase": phase, "step_idx": s, "layer_idx": l, "elapsed_ms": ms}
+                for phase, ledger in self._ledgers.items() for ms, s, l in ledger.settled]
+
+    def _csv_row_of(self, phase: str) -> Optional[str]:
+        if phase in self._CSV_ROW:
+            return self._CSV_ROW[phase]
+        if phase in self.DETAILED_PHASES or phase.startswith("flashinfer_residual_bucket_le"):
+            return phase
+        return None  # recorded for rows() only, as the reference's own extra phases
 
     def dump_csv(self, output_path: str, extra_totals: Optional[Dict[str, float]] = None
                  ) -> Dict[str, Dict[str, float]]:
-        """One aggregate row per phase (timing.py:97-218): ``top_k_selection``
-        (sum of ``topk_mask`` events), ``attention_execution``, the detailed
-        phases, any ``extra_totals``, then a ``residual_route_stats`` row when
-        metrics were recorded. Columns: phase, total_ms, calls, mean_ms and
-        the metric fields."""
-        totals: Dict[str, float] = {"top_k_selection": 0.0, "attention_execution": 0.0}
-        totals.update({p: 0.0 for p in self.DETAILED_PHASES})
-        calls: Dict[str, float] = {p: 0.0 for p in totals}
-        aliases = {"topk_mask": "top_k_selection", "attention_execution": "attention_execution"}
-        for row in self.rows():
-            raw = row["phase"]
-            phase = aliases.get(raw)
-            if phase is None and (raw in self.DETAILED_PHASES or raw.startswith("flashinfer_residual_bucket_le")):
-                phase = raw
-                totals.setdefault(phase, 0.0)
-                calls.setdefault(phase, 0.0)
-            if phase is None:
+        """Writes the reference's timing CSV (timing.py:97-218): rows
+        ``top_k_selection`` (the ``topk_mask`` spans), ``attention_execution``,
+        every detailed phase (zero calls when not recorded), then any bucket
+        phases seen, each ``extra_totals`` entry as one call, and a
+        ``residual_route_stats`` row when metrics were recorded. Columns:
+        phase, total_ms, calls, mean_ms and the metric fields. Returns
+        {row: {calls, total_ms, mean_ms}}."""
+        self._settle()
+        order = ["top_k_selection", "attention_execution", *self.DETAILED_PHASES]
+        acc: Dict[str, List[float]] = {row: [0.0, 0.0] for row in order}  # row -> [total_ms, calls]
+        for phase, ledger in self._ledgers.items():
+            row = self._csv_row_of(phase)
+            if row is None:
                 continue
-            totals[phase] += float(row["elapsed_ms"])
-            calls[phase] += 1.0
-        for phase, ms in (extra_totals or {}).items():
-            totals[phase] = float(ms)
-            calls[phase] = 1.0
+            slot = acc.setdefault(row, [0.0, 0.0])
+            slot[0] += ledger.total_ms()
+            slot[1] += len(ledger.settled)
+        for row, ms in (extra_totals or {}).items():
+            acc[row] = [float(ms), 1.0]
+        summary = {row: {"calls": n, "total_ms": t, "mean_ms": t / n if n else 0.0} for row, (t, n) in acc.items()}
+
+        header = ["phase", "total_ms", "calls", "mean_ms", *self.METRIC_FIELDS]
+        lines = [{"phase": row, "total_ms": s["total_ms"], "calls": int(s["calls"]), "mean_ms": s["mean_ms"]}
+                 for row, s in summary.items()]
+        per_field = {f: [snap[f] for snap in self._metric_snapshots if f in snap] for f in self.METRIC_FIELDS}
+        n_stats = max(len(v) for v in per_field.values())
+        if n_stats:
+            lines.append({"phase": "residual_route_stats", "total_ms": "", "calls": n_stats, "mean_ms": "",
+                          **{f: sum(v) / len(v) if v else float("nan") for f, v in per_field.items()}})
         os.makedirs(os.path.dirname(output_path) or ".", exist_ok=True)
         with open(output_path, "w", newline="") as fh:
-            wr = csv.DictWriter(fh, fieldnames=["phase", "total_ms", "calls", "mean_ms", *self.METRIC_FIELDS])
-            wr.writeheader()
-            for phase, total in totals.items():
-                n = calls.get(phase, 0.0)
-                wr.writerow({"phase": phase, "total_ms": total, "calls": int(n),
-                             "mean_ms": total / n if n else 0.0})
-            metrics = {name: self._metric_records.get(name, []) for name in self.METRIC_FIELDS}
-            n_metric = max((len(v) for v in metrics.values()), default=0)
-            if n_metric:
-                wr.writerow({"phase": "residual_route_stats", "total_ms": "", "calls": n_metric, "mean_ms": "",
-                             **{k: sum(v) / len(v) if v else float("nan") for k, v in metrics.items()}})
-        return {p: {"calls": calls.get(p, 0.0), "total_ms": t, "mean_ms": t / calls[p] if calls.get(p) else 0.0}
-                for p, t in totals.items()}
+            writer = csv.DictWriter(fh, fieldnames=header)
+            writer.writeheader()
+            writer.writerows(lines)
+        return summary

@@ -109,3 +109,85 @@ def test_cache_info_counts_reference_fields(module, per_entry):
     finally:
         cls._cached_metadata.clear()
         cls._cached_metadata.update(saved)
+
+
+def _hy_records(cls):
+    cls.density_records.clear()
+    cls.sparsity_records.clear()
+    for step, layer, dens in ((20, 3, 0.2), (20, 1, 0.4), (13, 0, 0.9)):
+        cls.density_records.setdefault(step, {})[layer] = dens
+    cls.sparsity_records.setdefault(20, {})[1] = {"block_density": 0.4, "final_density": 0.4,
+                                                  "residual_count_mean": 2.0, "fine_top_k": float("nan")}
+    cls.sparsity_records.setdefault(13, {})[0] = {"block_density": 0.9, "residual_count_mean": 4.0,
+                                                  "occupancy_histogram": [1] * 49}
+
+
+def test_hunyuan_density_records_format(tmp_path, capsys):
+    """The HunyuanVideo density table and CSV (attention_hyvideo.py:1511-1573):
+    rows in (step, layer) order, the overall mean 0.5 and the per-step mean
+    (0.9 + 0.3) / 2 = 0.6, and NaN where no route statistic was recorded."""
+    from dfsattn_amd.attention_hyvideo import DFS_Attention
+    _hy_records(DFS_Attention)
+    try:
+        path = DFS_Attention.dump_density_records(str(tmp_path / "x" / "density.csv"))
+        printed = capsys.readouterr().out.splitlines()
+        assert "===== DFS Attention actual density records =====" in printed
+        assert " step_idx  layer_idx   density  density%" in printed
+        assert "       13          0    0.9000     90.00" in printed
+        assert "Mean density over all layers/steps: 0.5000 (50.00%)" in printed
+        assert "Mean density per step (averaged over layers): 0.6000 (60.00%)" in printed
+        rows = list(csv.DictReader(open(path)))
+        assert list(rows[0])[:4] == ["step_idx", "layer_idx", "density", "residual_count_mean"]
+        assert list(rows[0])[-1] == "occupancy_histogram" and len(rows[0]) == 13
+        assert [(r["step_idx"], r["layer_idx"]) for r in rows] == [("13", "0"), ("20", "1"), ("20", "3")]
+        assert rows[1]["residual_count_mean"] == "2.0" and rows[2]["residual_count_mean"] == "nan"
+        sp = DFS_Attention.dump_sparsity_records(str(tmp_path / "sp.csv"))
+        srows = list(csv.DictReader(open(sp)))
+        assert list(srows[0])[:3] == ["step_idx", "layer_idx", "p_mass"] and list(srows[0])[-1] == "final_hybrid_sparsity"
+        assert len(srows) == 2 and srows[0]["block_density"] == "0.9" and srows[0]["final_density"] == "nan"
+    finally:
+        DFS_Attention.density_records.clear()
+        DFS_Attention.sparsity_records.clear()
+
+
+def test_hunyuan_density_summary_appends(tmp_path):
+    """One row per prompt (attention_hyvideo.py:1575-1691): the per-step mean
+    of layer means, the record mean, counts, finite route-statistic means,
+    the summed occupancy histogram; later prompts append; an old
+    metric,value file becomes a row; a foreign header is refused."""
+    from dfsattn_amd.attention_hyvideo import DFS_Attention
+    _hy_records(DFS_Attention)
+    out = tmp_path / "density_summary.csv"
+    try:
+        DFS_Attention.dump_density_summary(str(out), prompt_idx=0, prompt="a cat")
+        DFS_Attention.dump_density_summary(str(out), prompt_idx=1, prompt="a dog")
+        rows = list(csv.DictReader(open(out)))
+        assert [r["prompt"] for r in rows] == ["a cat", "a dog"]
+        r = rows[0]
+        assert float(r["mean_final_density_sparse_steps_avg_over_layers"]) == pytest.approx(0.6)
+        assert float(r["mean_density_per_sparse_step"]) == pytest.approx(0.6)
+        assert float(r["mean_density_over_sparse_step_layer_records"]) == pytest.approx(0.5)
+        assert (r["num_sparse_step_layer_records"], r["num_sparse_steps"], r["num_layers_with_records"]) == ("3", "2", "3")
+        assert float(r["mean_residual_count_mean"]) == 3.0 and r["mean_fine_top_k"] == "nan"
+        assert r["occupancy_histogram"] == str(tuple([1] * 49))
+        legacy = tmp_path / "legacy.csv"
+        legacy.write_text("metric,value\nmean_density_per_sparse_step,0.25\nnum_sparse_steps,7\n")
+        DFS_Attention.dump_density_summary(str(legacy), prompt_idx=2)
+        lrows = list(csv.DictReader(open(legacy)))
+        assert len(lrows) == 2 and lrows[0]["mean_density_per_sparse_step"] == "0.25" and lrows[0]["prompt"] == ""
+        bad = tmp_path / "bad.csv"
+        bad.write_text("foo,bar\n1,2\n")
+        with pytest.raises(ValueError):
+            DFS_Attention.dump_density_summary(str(bad))
+    finally:
+        DFS_Attention.density_records.clear()
+        DFS_Attention.sparsity_records.clear()
+    assert DFS_Attention.dump_density_summary(str(out)) is None  # nothing recorded
+
+
+def test_hunyuan_subblock_profile_api():
+    from dfsattn_amd.attention_hyvideo import DFS_Attention
+    DFS_Attention.configure_subblock_retention_profile(None)
+    assert DFS_Attention.dump_subblock_retention_profile() is None
+    with pytest.raises(NotImplementedError):
+        DFS_Attention.configure_subblock_retention_profile("/tmp/x", (0.9,))
