@@ -17,6 +17,7 @@
 #include <math.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "lds_copy.h"
@@ -307,7 +308,12 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
   constexpr int ROWS = 32;               // key tiles per chunk
   constexpr int TILE = ROWS * D;         // uint16 elements of one hi (or lo) chunk
   constexpr int LOADS = ROWS * D * 2 / 4096;  // 16-byte loads per thread per hi (or lo) chunk
-  __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][2][TILE];  // [buffer][hi, lo]
+  // The two key-chunk buffers are separate LDS objects ([hi, lo] each), and
+  // every chunk step knows its buffer at compile time: the compiler then sees
+  // that the copy into one buffer cannot alias the reads of the other and
+  // does not wait for the copy in flight before reading the current chunk.
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf0[2][TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t kbuf1[2][TILE];
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const Policy& pol = p.pol;
   const int h = blockIdx.y;
@@ -339,17 +345,33 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     const int ws = __builtin_amdgcn_readfirstlane(w);
     const TileCopy<D * 2> copy(ws, lane);
     constexpr uint32_t CHUNK_BYTES = ROWS * D * 2;
-    auto issue = [&](int step) {
+    // Step s (s < nchunks: chunk s; in pass 2 of the two-pass form, chunk
+    // s - nchunks) reads buffer s & 1; the buffer is a template argument.
+    constexpr std::integral_constant<int, 0> B0{};
+    constexpr std::integral_constant<int, 1> B1{};
+    auto issue = [&](int step, auto buf) {
       // Past the last step the copy reloads chunk 0 into the buffer nobody
       // reads any more, so the wait count stays fixed and every load stays in
       // range.
+      uint16_t(&kb)[2][TILE] = decltype(buf)::value ? kbuf1 : kbuf0;
       const int c = step < 2 * nchunks ? (step < nchunks ? step : step - nchunks) : 0;
-      copy.template issue<LOADS>(hrs, c * CHUNK_BYTES, &kbuf[step & 1][0][0], ws);
-      copy.template issue<LOADS>(lrs, c * CHUNK_BYTES, &kbuf[step & 1][1][0], ws);
+      copy.template issue<LOADS>(hrs, c * CHUNK_BYTES, &kb[0][0], ws);
+      copy.template issue<LOADS>(lrs, c * CHUNK_BYTES, &kb[1][0], ws);
     };
-    auto chunk_scores = [&](int buf) {
-      const uint16_t* kh = &kbuf[buf][0][0];
-      const uint16_t* kl = &kbuf[buf][1][0];
+    // fn(s, buffer of s) for s in [s0, s1), buffers as compile-time constants.
+    auto for_steps = [&](int s0, int s1, auto fn) {
+      int st = s0;
+      if ((st & 1) && st < s1) fn(st++, B1);
+      for (; st + 1 < s1; st += 2) {
+        fn(st, B0);
+        fn(st + 1, B1);
+      }
+      if (st < s1) fn(st, B0);
+    };
+    auto chunk_scores = [&](auto buf) {
+      uint16_t(&kb)[2][TILE] = decltype(buf)::value ? kbuf1 : kbuf0;
+      const uint16_t* kh = &kb[0][0];
+      const uint16_t* kl = &kb[1][0];
       f32x16 acc = {};
 #pragma unroll
       for (int ds = 0; ds < D / 16; ++ds) {
@@ -362,7 +384,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       return acc;
     };
 
-    issue(0);
+    issue(0, B0);
     if constexpr (ONE_PASS) {
       // One pass: exp2(s - m) against a reference m shared by the two lane
       // halves of a query tile (the first chunk's maximum; moved only when a
@@ -379,12 +401,12 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       auto U = [&](int kb) -> float& { return ubase[static_cast<int64_t>(kb) * WG_TILES]; };
       constexpr int BPC = ROWS / TPB;  // key blocks per chunk
       float m = -INFINITY, z = 0.f;
-      for (int c = 0; c < nchunks; ++c) {
+      for_steps(0, nchunks, [&](int c, auto buf) {
         wait_vmcnt_0();
         block_barrier();
-        issue(c + 1);
-        if (!wave_scores) continue;
-        const f32x16 acc = chunk_scores(c & 1);
+        issue(c + 1, std::integral_constant<int, 1 - decltype(buf)::value>{});
+        if (!wave_scores) return;
+        const f32x16 acc = chunk_scores(buf);
         const int lim = (c + 1) * ROWS <= p.k_tiles ? ROWS : p.k_tiles - c * ROWS;  // valid key tiles
         auto joint_max = [&]() {
           float cm = -INFINITY;
@@ -433,7 +455,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
           for (int gg = 0; gg < 4; ++gg)
             U(c * 8 + 2 * gg + hl) = (pr[4 * gg] + pr[4 * gg + 1]) + (pr[4 * gg + 2] + pr[4 * gg + 3]);
         }
-      }
+      });
       wait_vmcnt_0();  // the trailing (empty) copies have retired
       if (wave_scores) {
         const float Z = z + __shfl_xor(z, 32);  // same reference in both halves
@@ -467,12 +489,12 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     // to 2^-126 nothing of weight is lost and no block sum can overflow.
     // Only the last chunk can hold key tiles past the end.
     float m = -INFINITY, z = 0.f;
-    for (int c = 0; c < nchunks; ++c) {
+    for_steps(0, nchunks, [&](int c, auto buf) {
       wait_vmcnt_0();
       block_barrier();
-      issue(c + 1);
+      issue(c + 1, std::integral_constant<int, 1 - decltype(buf)::value>{});
       if (wave_scores) {
-        const f32x16 acc = chunk_scores(c & 1);
+        const f32x16 acc = chunk_scores(buf);
         const int lim = (c + 1) * ROWS <= p.k_tiles ? ROWS : p.k_tiles - c * ROWS;  // valid key tiles
         auto masked_max = [&]() {
           float cm = -INFINITY;
@@ -505,7 +527,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
           z += sum;
         }
       }
-    }
+    });
     // Combine the two lane halves (same query tile, different key tiles).
     const float m_o = __shfl_xor(m, 32), z_o = __shfl_xor(z, 32);
     const float M = fmaxf(m, m_o);
@@ -515,13 +537,13 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     const float invZ = Z > 0.f ? 1.0f / Z : 0.f;
 
     // Pass 2: tile probabilities summed into 128x128 blocks.
-    for (int c = 0; c < nchunks; ++c) {
-      const int step = nchunks + c;
+    for_steps(nchunks, 2 * nchunks, [&](int step, auto buf) {
+      const int c = step - nchunks;
       wait_vmcnt_0();
       block_barrier();
-      issue(step + 1);
-      if (!wave_scores) continue;
-      const f32x16 acc = chunk_scores(step & 1);
+      issue(step + 1, std::integral_constant<int, 1 - decltype(buf)::value>{});
+      if (!wave_scores) return;
+      const f32x16 acc = chunk_scores(buf);
       float pr[16];
       if ((c + 1) * ROWS <= p.k_tiles) {
 #pragma unroll
@@ -558,7 +580,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
           if ((l32 & 3) == 0 && kbk < pol.Kb && (!GB || qb0 + g < pol.scored_rows)) bsum[g * pol.Kb + kbk] = sum;
         }
       }
-    }
+    });
     wait_vmcnt_0();  // the trailing (empty) copies have retired
     __syncthreads();  // with GB: the block sums in global memory are visible to the workgroup
     }
