@@ -162,6 +162,47 @@ __device__ __forceinline__ f32x16 score_chunk(const ScoreParams& p, int h, int c
   return acc;
 }
 
+// Query fragments of one lane (tile l32, dims hl*8.. of every 16) as
+// q' = (q_hi + q_lo) * scale * log2(e) in fp32, split again into bf16 hi/lo:
+// the products then arrive in log2 units with no per-score multiply, and the
+// split keeps them fp32-accurate.
+template <int D>
+__device__ __forceinline__ void load_q_prescaled(const ScoreParams& p, bool valid, int64_t base, bf16x8* qh,
+                                                 bf16x8* ql) {
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds) {
+    const uint4 h4 = valid ? p.q_hi[base + 2 * ds] : make_uint4(0, 0, 0, 0);
+    const uint4 l4 = valid ? p.q_lo[base + 2 * ds] : make_uint4(0, 0, 0, 0);
+    uint32_t hb[8], lb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = (bf16_bits_to_f32(u16_at(h4, i)) + bf16_bits_to_f32(u16_at(l4, i))) * p.scale_log2;
+      hb[i] = f32_to_bf16_bits(x);
+      lb[i] = f32_to_bf16_bits(x - bf16_bits_to_f32(hb[i]));
+    }
+    qh[ds] = __builtin_bit_cast(bf16x8, make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16),
+                                                   hb[4] | (hb[5] << 16), hb[6] | (hb[7] << 16)));
+    ql[ds] = __builtin_bit_cast(bf16x8, make_uint4(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16),
+                                                   lb[4] | (lb[5] << 16), lb[6] | (lb[7] << 16)));
+  }
+}
+
+// Exchanges between the two lane halves (lane ^ 32) by v_permlane32_swap.
+__device__ __forceinline__ float xhalf_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ int xhalf_or(int v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+  return static_cast<int>(r[0] | r[1]);
+}
+// Lanes of half 0 get a + a', lanes of half 1 get b + b' (primes: the value
+// of the same lane in the other half).
+__device__ __forceinline__ float xhalf_pair_sum(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Key-tile row held in accumulator register r by lane half hl (32x32 MFMA
 // output layout).
 __device__ __forceinline__ int acc_row(int r, int hl) { return (r >> 2) * 8 + hl * 4 + (r & 3); }
@@ -191,11 +232,7 @@ __global__ void __launch_bounds__(256) score_topk_kernel(ScoreParams p) {
     const int qt = qb0 * TPB + l32;
     const bool qv = qt < p.q_tiles;
     const int64_t qbase = (static_cast<int64_t>(h) * p.q_tiles + (qv ? qt : 0)) * CPR + hl;
-#pragma unroll
-    for (int ds = 0; ds < D / 16; ++ds) {
-      qh[ds] = __builtin_bit_cast(bf16x8, qv ? p.q_hi[qbase + 2 * ds] : make_uint4(0, 0, 0, 0));
-      ql[ds] = __builtin_bit_cast(bf16x8, qv ? p.q_lo[qbase + 2 * ds] : make_uint4(0, 0, 0, 0));
-    }
+    load_q_prescaled<D>(p, qv, qbase, qh, ql);
     const int nchunks = (p.k_tiles + 31) / 32;
 
     // Pass 1: running max and normaliser (log2 domain) of every query tile.
@@ -207,7 +244,7 @@ __global__ void __launch_bounds__(256) score_topk_kernel(ScoreParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const bool kv = c * 32 + acc_row(r, hl) < p.k_tiles;
-        t[r] = kv ? acc[r] * p.scale_log2 : -INFINITY;
+        t[r] = kv ? acc[r] : -INFINITY;
         cm = fmaxf(cm, t[r]);
       }
       const float mn = fmaxf(m, cm);
@@ -240,7 +277,7 @@ __global__ void __launch_bounds__(256) score_topk_kernel(ScoreParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const bool kv = c * 32 + acc_row(r, hl) < p.k_tiles;
-        pr[r] = kv ? exp2_fast(acc[r] * p.scale_log2 - M) * invZ : 0.f;
+        pr[r] = kv ? exp2_fast(acc[r] - M) * invZ : 0.f;
       }
       if constexpr (TPB == 8) {
         // Register group r/4 = key block b of the chunk; halves hold the
@@ -330,11 +367,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     const int qt = qbw * TPB + l32;
     const bool qv = qt < p.q_tiles;
     const int64_t qbase = (static_cast<int64_t>(h) * p.q_tiles + (qv ? qt : 0)) * CPR + hl;
-#pragma unroll
-    for (int ds = 0; ds < D / 16; ++ds) {
-      qh[ds] = __builtin_bit_cast(bf16x8, qv ? p.q_hi[qbase + 2 * ds] : make_uint4(0, 0, 0, 0));
-      ql[ds] = __builtin_bit_cast(bf16x8, qv ? p.q_lo[qbase + 2 * ds] : make_uint4(0, 0, 0, 0));
-    }
+    load_q_prescaled<D>(p, qv, qbase, qh, ql);
 #pragma unroll
     for (int ds = 0; ds < D / 16; ++ds) asm volatile("" ::"v"(qh[ds]), "v"(ql[ds]));
     const bool wave_scores = qbw < score_rows;
@@ -368,19 +401,39 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       }
       if (st < s1) fn(st, B0);
     };
+    // S'^T chunk (32 key tiles x 32 query tiles) on the hi/lo split, Q
+    // prescaled so S' is in log2 units. The two K operand reads of step ds + 1
+    // are issued before the three MFMAs of step ds (pinned by scheduling-group
+    // barriers), so their LDS latency runs under those MFMAs.
     auto chunk_scores = [&](auto buf) {
       uint16_t(&kb)[2][TILE] = decltype(buf)::value ? kbuf1 : kbuf0;
       const uint16_t* kh = &kb[0][0];
       const uint16_t* kl = &kb[1][0];
+      constexpr int DS = D / 16;
+      uint4 ah[2], al[2];
+      ah[0] = lds_chunk<CPR>(kh, l32, hl);
+      al[0] = lds_chunk<CPR>(kl, l32, hl);
       f32x16 acc = {};
 #pragma unroll
-      for (int ds = 0; ds < D / 16; ++ds) {
-        const bf16x8 ah = __builtin_bit_cast(bf16x8, lds_chunk<CPR>(kh, l32, ds * 2 + hl));
-        const bf16x8 al = __builtin_bit_cast(bf16x8, lds_chunk<CPR>(kl, l32, ds * 2 + hl));
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[ds], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[ds], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[ds], acc, 0, 0, 0);
+      for (int ds = 0; ds < DS; ++ds) {
+        if (ds + 1 < DS) {
+          ah[(ds + 1) & 1] = lds_chunk<CPR>(kh, l32, (ds + 1) * 2 + hl);
+          al[(ds + 1) & 1] = lds_chunk<CPR>(kl, l32, (ds + 1) * 2 + hl);
+        }
+        const bf16x8 a = __builtin_bit_cast(bf16x8, ah[ds & 1]);
+        const bf16x8 b = __builtin_bit_cast(bf16x8, al[ds & 1]);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qh[ds], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, ql[ds], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, qh[ds], acc, 0, 0, 0);
       }
+      constexpr int kMfma = 0x008, kDsRead = 0x100;
+      __builtin_amdgcn_sched_group_barrier(kDsRead, 2, 0);
+#pragma unroll
+      for (int ds = 0; ds + 1 < DS; ++ds) {
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kMfma, 3, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kMfma, 3, 0);
       return acc;
     };
 
@@ -400,35 +453,54 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
                            (static_cast<int64_t>(h) * gridDim.x + blockIdx.x) * p.tile_cols * WG_TILES + w * 32 + l32;
       auto U = [&](int kb) -> float& { return ubase[static_cast<int64_t>(kb) * WG_TILES]; };
       constexpr int BPC = ROWS / TPB;  // key blocks per chunk
+      constexpr int NST = BPC / 2;     // key-block sums one lane stores per chunk
+      // Workspace column of pending sum j of chunk c for this lane.
+      auto st_col = [&](int c, int j) { return TPB == 8 ? c * 4 + 2 * hl + j : c * 8 + 2 * j + hl; };
       float m = -INFINITY, z = 0.f;
+      float pend[NST];  // this lane's sums of the previous chunk, stored one step late
+      // A chunk's sums are stored after the next chunk's barrier and copy
+      // issue, so the wait for that copy at the top of a step does not also
+      // wait for stores issued just before it.
+      auto flush = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < NST; ++j) U(st_col(c, j)) = pend[j];
+      };
       for_steps(0, nchunks, [&](int c, auto buf) {
         wait_vmcnt_0();
         block_barrier();
         issue(c + 1, std::integral_constant<int, 1 - decltype(buf)::value>{});
         if (!wave_scores) return;
-        const f32x16 acc = chunk_scores(buf);
+        if (c > 0) flush(c - 1);
+        __builtin_amdgcn_sched_barrier(0);  // the stores stay ahead of this chunk's MFMAs
+        const f32x16 acc = chunk_scores(buf);  // s' (log2 units)
         const int lim = (c + 1) * ROWS <= p.k_tiles ? ROWS : p.k_tiles - c * ROWS;  // valid key tiles
         auto joint_max = [&]() {
           float cm = -INFINITY;
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (acc_row(r, hl) < lim) cm = fmaxf(cm, acc[r] * p.scale_log2);
-          return fmaxf(cm, __shfl_xor(cm, 32));
+            if (acc_row(r, hl) < lim) cm = fmaxf(cm, acc[r]);
+          return xhalf_max(cm);
         };
-        float pr[16];
-        auto exps = [&]() {
-          float sum = 0.f;
+        // exp2(s' - ref) summed over the four key tiles of register group b
+        // (u[b]); returns this lane's sum over all its key tiles. Only the
+        // last chunk can hold key tiles past the end.
+        float u[4];
+        auto sums = [&](float ref) {
+          float pr[16];
+          if (lim == ROWS) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            pr[r] = acc_row(r, hl) < lim ? exp2_fast(fmaf(acc[r], p.scale_log2, -m)) : 0.f;
-            sum += pr[r];
+            for (int r = 0; r < 16; ++r) pr[r] = exp2_fast(acc[r] - ref);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pr[r] = acc_row(r, hl) < lim ? exp2_fast(acc[r] - ref) : 0.f;
           }
-          return sum;
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) u[g4] = (pr[4 * g4] + pr[4 * g4 + 1]) + (pr[4 * g4 + 2] + pr[4 * g4 + 3]);
+          return (u[0] + u[1]) + (u[2] + u[3]);
         };
         if (!(m > -INFINITY)) m = joint_max();  // the first chunk with valid keys
-        float sum = exps();
-        int ovf = !(sum <= 0x1p64f);
-        ovf |= __shfl_xor(ovf, 32);
+        float sum = sums(m);
+        const int ovf = xhalf_or(!(sum <= 0x1p64f));
         if (__any(ovf)) {
           if (ovf) {  // a logit far above the reference: move it to this chunk's maximum
             const float mn = fmaxf(m, joint_max());
@@ -438,24 +510,21 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
             for (int j = hl; j < c * BPC; j += 2) U(j) *= f;
             m = mn;
           }
-          sum = exps();
+          sum = sums(m);
         }
         z += sum;
         if constexpr (TPB == 8) {
-          float u[4];
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            u[b] = (pr[4 * b] + pr[4 * b + 1]) + (pr[4 * b + 2] + pr[4 * b + 3]);
-            u[b] += __shfl_xor(u[b], 32);
-          }
-          U(c * 4 + 2 * hl) = hl ? u[2] : u[0];  // the two halves store two key blocks each
-          U(c * 4 + 2 * hl + 1) = hl ? u[3] : u[1];
+          // Register group b holds key block b of the chunk, its 8 key tiles
+          // split over the two lane halves: half 0 keeps blocks 0, 1 and
+          // half 1 blocks 2, 3, each summed over both halves.
+          pend[0] = xhalf_pair_sum(u[0], u[2]);
+          pend[1] = xhalf_pair_sum(u[1], u[3]);
         } else {
 #pragma unroll
-          for (int gg = 0; gg < 4; ++gg)
-            U(c * 8 + 2 * gg + hl) = (pr[4 * gg] + pr[4 * gg + 1]) + (pr[4 * gg + 2] + pr[4 * gg + 3]);
+          for (int j = 0; j < NST; ++j) pend[j] = u[j];  // group j, half hl: key block 2j + hl
         }
       });
+      if (wave_scores && nchunks > 0) flush(nchunks - 1);
       wait_vmcnt_0();  // the trailing (empty) copies have retired
       if (wave_scores) {
         const float Z = z + __shfl_xor(z, 32);  // same reference in both halves
@@ -500,18 +569,18 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
           float cm = -INFINITY;
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (acc_row(r, hl) < lim) cm = fmaxf(cm, acc[r] * p.scale_log2);
+            if (acc_row(r, hl) < lim) cm = fmaxf(cm, acc[r]);
           return cm;
         };
         auto exp_sum = [&](float ref) {
           float sum = 0.f;
           if (lim == ROWS) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sum += exp2_fast(fmaf(acc[r], p.scale_log2, -ref));
+            for (int r = 0; r < 16; ++r) sum += exp2_fast(acc[r] - ref);
           } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-              if (acc_row(r, hl) < lim) sum += exp2_fast(fmaf(acc[r], p.scale_log2, -ref));
+              if (acc_row(r, hl) < lim) sum += exp2_fast(acc[r] - ref);
           }
           return sum;
         };
@@ -547,11 +616,11 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       float pr[16];
       if ((c + 1) * ROWS <= p.k_tiles) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pr[r] = exp2_fast(fmaf(acc[r], p.scale_log2, -M));
+        for (int r = 0; r < 16; ++r) pr[r] = exp2_fast(acc[r] - M);
       } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          pr[r] = c * ROWS + acc_row(r, hl) < p.k_tiles ? exp2_fast(fmaf(acc[r], p.scale_log2, -M)) : 0.f;
+          pr[r] = c * ROWS + acc_row(r, hl) < p.k_tiles ? exp2_fast(acc[r] - M) : 0.f;
       }
       // exp2(s - M) summed over a query tile's key tiles of the block, scaled
       // by that tile's 1/Z, then summed over the block's query tiles
