@@ -48,7 +48,7 @@ __device__ __forceinline__ uint64_t lanes_below(int lane) {
 //  * columns [dense_col, kb): always kept.
 // cols receives the kept columns in ascending order; mask_row (optional) the
 // uint8 mask. hist is 256 words of wave-private LDS.
-__device__ void select_row(const float* scores, int n_cand, int k_pick, int dense_col, int kb,
+__device__ __forceinline__ void select_row(const float* scores, int n_cand, int k_pick, int dense_col, int kb,
                            int32_t* cols, uint8_t* mask_row, uint32_t* hist, int lane) {
   uint32_t prefix = 0, pmask = 0;
   int remaining = k_pick;
@@ -191,6 +191,10 @@ __device__ __forceinline__ void load_q_prescaled(const ScoreParams& p, bool vali
 __device__ __forceinline__ float xhalf_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 __device__ __forceinline__ int xhalf_or(int v) {
   const auto r = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
@@ -351,12 +355,15 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
   // does not wait for the copy in flight before reading the current chunk.
   __shared__ __attribute__((aligned(16))) uint16_t kbuf0[2][TILE];
   __shared__ __attribute__((aligned(16))) uint16_t kbuf1[2][TILE];
+  __shared__ float inv_z[ONE_PASS ? 128 : 1];  // one pass: 1/Z of the workgroup's query tiles
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const Policy& pol = p.pol;
   const int h = blockIdx.y;
   const int qb0 = blockIdx.x * G;
   // [G][Kb] block sums of this workgroup's query blocks
-  float* bsum = GB ? p.scores_out + (static_cast<int64_t>(h) * pol.scored_rows + qb0) * pol.Kb : smem;
+  float* bsum = GB ? (p.scores_out ? p.scores_out + (static_cast<int64_t>(h) * pol.scored_rows + qb0) * pol.Kb
+                                   : nullptr)
+                   : smem;
   uint32_t* hist = reinterpret_cast<uint32_t*>(GB ? smem : smem + G * pol.Kb);  // [4][256]
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int score_rows = p.scores_out ? pol.scored_rows : min(pol.scored_rows, pol.dense_row);
@@ -525,30 +532,13 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
         }
       });
       if (wave_scores && nchunks > 0) flush(nchunks - 1);
-      wait_vmcnt_0();  // the trailing (empty) copies have retired
+      wait_vmcnt_0();  // the trailing (empty) copies and the last sums have retired
       if (wave_scores) {
-        const float Z = z + __shfl_xor(z, 32);  // same reference in both halves
-        const float invZ = Z > 0.f ? 1.0f / Z : 0.f;
-        __threadfence_block();  // the rows written above are visible to the wave's loads
-        // Block sums: lane (tile l32, half hl) scales 4 columns of its row,
-        // then the TPB tiles of a query block are summed by shuffles.
-        for (int kb0 = hl * 4; kb0 < nchunks * BPC; kb0 += 8) {
-          float v[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) v[j] = U(kb0 + j) * invZ;
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int off = 1; off < TPB; off <<= 1) v[j] += __shfl_xor(v[j], off);
-          const int g = w * QBW + l32 / TPB;
-          if ((l32 & (TPB - 1)) == 0 && (!GB || qb0 + g < pol.scored_rows)) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (kb0 + j < pol.Kb) bsum[g * pol.Kb + kb0 + j] = v[j];
-          }
-        }
+        const float Z = xhalf_sum(z);  // same reference in both halves
+        if (hl == 0) inv_z[w * 32 + l32] = Z > 0.f ? 1.0f / Z : 0.f;
       }
-      __syncthreads();  // the block sums are visible to the workgroup
+      __threadfence_block();  // the workspace rows written above are visible to the workgroup's loads
+      __syncthreads();        // inv_z is written and no wave reads the key chunks any more
     } else {
     // Pass 1: normaliser z of every query tile (one per lane half) against a
     // reference m in the log2 domain: m is the maximum of the tile's first
@@ -663,17 +653,59 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     }
   }
 
+  // One pass: the block sums of a row, sum over its TPB query tiles of
+  // (workspace sum) / Z, go to a wave-private LDS row in the key-chunk
+  // buffers (free now; ROW_CAP columns per wave) and to scores_out when the
+  // caller asked for scores; the selection reads the LDS row.
+  constexpr int ROW_CAP = TILE / 2;  // floats: each key-chunk buffer (2 x TILE uint16) holds two waves' rows
+  float* const rowbuf = reinterpret_cast<float*>(w < 2 ? &kbuf0[0][0] : &kbuf1[0][0]) + (w & 1) * ROW_CAP;
   for (int g = 0; g < QBW; ++g) {
     const int qb = qbw + g;
     if (qb >= pol.Qb) break;
     const int64_t row = static_cast<int64_t>(h) * pol.Qb + qb;
     int32_t* cols = p.col_idx + p.row_ptr[row];
     uint8_t* mrow = p.mask_out ? p.mask_out + row * pol.Kb : nullptr;
-    if (qb >= pol.dense_row || qb >= pol.scored_rows)
-      dense_row(pol.Kb, cols, mrow, lane);
-    else
-      select_row(bsum + (w * QBW + g) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow,
-                 hist + w * 256, lane);
+    const bool dense = qb >= pol.dense_row || qb >= pol.scored_rows;
+    if constexpr (ONE_PASS) {
+      if (qb < score_rows) {
+        constexpr int WG_TILES = G * TPB;
+        float iz[TPB];
+#pragma unroll
+        for (int i = 0; i < TPB; ++i) iz[i] = inv_z[w * 32 + g * TPB + i];
+        const float* src = p.tile_sums + (static_cast<int64_t>(h) * gridDim.x + blockIdx.x) * p.tile_cols * WG_TILES +
+                           w * 32 + g * TPB;
+        float* out = p.scores_out ? p.scores_out + (static_cast<int64_t>(h) * pol.scored_rows + qb) * pol.Kb : nullptr;
+#pragma unroll 4
+        for (int kb = lane; kb < pol.Kb; kb += kWave) {
+          const float4* u = reinterpret_cast<const float4*>(src + static_cast<int64_t>(kb) * WG_TILES);
+          float t[8];
+          const float4 a = u[0];
+          t[0] = a.x * iz[0]; t[1] = a.y * iz[1]; t[2] = a.z * iz[2]; t[3] = a.w * iz[3];
+          float v;
+          if constexpr (TPB == 8) {
+            const float4 b4 = u[1];
+            t[4] = b4.x * iz[4]; t[5] = b4.y * iz[5]; t[6] = b4.z * iz[6]; t[7] = b4.w * iz[7];
+            v = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+          } else {
+            v = (t[0] + t[1]) + (t[2] + t[3]);
+          }
+          rowbuf[kb] = v;
+          if (out) out[kb] = v;
+        }
+        lds_sync_wave();
+      }
+      if (dense)
+        dense_row(pol.Kb, cols, mrow, lane);
+      else
+        select_row(rowbuf, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow, hist + w * 256, lane);
+      lds_sync_wave();  // the next row may overwrite rowbuf
+    } else {
+      if (dense)
+        dense_row(pol.Kb, cols, mrow, lane);
+      else
+        select_row(bsum + (w * QBW + g) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow,
+                   hist + w * 256, lane);
+    }
   }
 }
 
@@ -802,8 +834,11 @@ int score_topk_impl(const char* name, const uint16_t* q_pool_hi, const uint16_t*
   p.k_tiles = static_cast<int>(k_blocks * tpb);
   p.scale_log2 = static_cast<float>(1.4426950408889634 / sqrt(static_cast<double>(head_dim)));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (workspace) {
-    DFS_REQUIRE(global_sums, "%s: the one-pass form (workspace given) needs scores_out", name);
+  // The one-pass form keeps one block-sum row per wave in its key-chunk
+  // buffers (2048 columns at head_dim 128, 1024 at 64); wider rows take the
+  // two-pass form.
+  const int64_t row_cap = 32 * head_dim / 2;
+  if (workspace && k_blocks <= row_cap) {
     const int64_t need = dfs_block_score_topk_workspace_size(heads, tile_size, q_blocks, k_blocks);
     DFS_REQUIRE(workspace_bytes >= need, "%s: workspace of %lld bytes, %lld needed", name,
                 (long long)workspace_bytes, (long long)need);

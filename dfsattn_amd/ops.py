@@ -193,11 +193,13 @@ def score_workspace_bytes(heads: int, tile: int, q_blocks: int, k_blocks: int) -
 def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
                      want_scores: bool = False, want_mask: bool = False, one_pass: bool = True):
     """Scores + top-k: returns (col_idx int32 [nnz], scores fp32 [H,Vb,Kb] or
-    None, mask uint8 [H,Qb,Kb] or None). The score matrix is always passed
-    to the kernel, which then keeps its block sums there rather than in LDS
-    (more workgroups per CU). With ``one_pass`` a workspace of per-tile
-    partial sums lets the kernel score every tile pair once instead of twice
-    (normaliser pass, then block-sum pass)."""
+    None, mask uint8 [H,Qb,Kb] or None). With ``one_pass`` a workspace of
+    per-tile partial sums lets the kernel score every tile pair once instead
+    of twice (normaliser pass, then block-sum pass), and the score matrix is
+    written only when asked for. The two-pass form (and rows wider than the
+    one-pass form's 16 * head_dim columns) always gets the score matrix,
+    where it keeps its block sums rather than in LDS (more workgroups per
+    CU)."""
     if prep.q_hi is None:
         raise ValueError("prepare_qkv was called without pooling")
     _require_device(prep.q_hi, row_ptr)
@@ -207,11 +209,13 @@ def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
     dev = prep.q_perm.device
     nnz = policy.nnz(prep.heads)
     col_idx = torch.empty(nnz, dtype=torch.int32, device=dev)
-    scores = torch.empty((prep.heads, policy.scored_rows, policy.k_blocks), dtype=torch.float32, device=dev)
+    one_pass_rows = one_pass and policy.k_blocks <= 16 * prep.head_dim
+    scores = (torch.empty((prep.heads, policy.scored_rows, policy.k_blocks), dtype=torch.float32, device=dev)
+              if want_scores or not one_pass_rows else None)
     mask = (torch.empty((prep.heads, policy.q_blocks, policy.k_blocks), dtype=torch.uint8, device=dev)
             if want_mask else None)
     ws, ws_bytes = None, 0
-    if one_pass:
+    if one_pass_rows:
         ws_bytes = score_workspace_bytes(prep.heads, prep.layout.tile, policy.q_blocks, policy.k_blocks)
         ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
     _lib.call("dfs_block_score_topk", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi), _ptr(prep.k_lo),

@@ -132,16 +132,17 @@ int dfs_prepare_fixup(const void* q, const void* k, const void* v,
  *   dense_row    rows dense_row..Qb-1 keep every column.
  *   row_ptr      CSR row offsets [H*Qb+1] consistent with the policy.
  *   col_idx      CSR columns (ascending per row).
- *   scores_out   optional fp32 [H][scored_rows][Kb] block scores. When
- *                given, the kernel accumulates its block sums there instead
- *                of in LDS, which lets more workgroups share a CU (faster;
- *                rows from dense_row on are then scored too).
+ *   scores_out   optional fp32 [H][scored_rows][Kb] block scores (rows from
+ *                dense_row on are then scored too). Without a workspace the
+ *                kernel accumulates its block sums there instead of in LDS,
+ *                which lets more workgroups share a CU (faster).
  *   mask_out     optional uint8 [H][Qb][Kb] block mask.
  *   workspace    optional device buffer of workspace_bytes >= the size from
- *                dfs_block_score_topk_workspace_size (16-byte aligned; needs
- *                scores_out). With it the kernel scores every tile pair once,
- *                keeping unnormalised per-tile block sums there, instead of
- *                twice (a normaliser pass, then a block-sum pass).
+ *                dfs_block_score_topk_workspace_size (16-byte aligned). With
+ *                it, and Kb <= 16 * head_dim, the kernel scores every tile
+ *                pair once, keeping unnormalised per-tile block sums there,
+ *                instead of twice (a normaliser pass, then a block-sum
+ *                pass); scores_out is then only written, not needed.
  * Ties are broken by (score descending, column ascending).
  * Replaces _compute_tile_score + _compute_block_mask
  * (attention_wan.py:157-261; attention_hyvideo.py:310-501).

@@ -269,7 +269,8 @@ def test_block_score_topk_lds_sums_path_selects_the_same(dev, video, text):
 
 
 def test_block_score_topk_workspace_checks(dev):
-    """The one-pass form needs a large enough, aligned workspace and a score matrix."""
+    """The one-pass form needs a large enough, aligned workspace; the score
+    matrix is optional there, and the selection is the same without it."""
     import ctypes
     from dfsattn_amd import _lib
     from dfsattn_amd.ops import _policy_args, score_workspace_bytes
@@ -289,13 +290,17 @@ def test_block_score_topk_workspace_checks(dev):
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     args = (p(prep.q_hi), p(prep.q_lo), p(prep.k_hi), p(prep.k_lo), heads, 64, 16, *_policy_args(pol), p(row_ptr),
             p(col))
-    for sc, w, nbytes in ((p(scores), p(ws), need - 4), (None, p(ws), need),
-                          (p(scores), ctypes.c_void_p(ws.data_ptr() + 4), need)):
+    for sc, w, nbytes in ((p(scores), p(ws), need - 4), (p(scores), ctypes.c_void_p(ws.data_ptr() + 4), need)):
         with pytest.raises(_lib.DfsKernelError):
             _lib.call("dfs_block_score_topk", *args, sc, None, w, nbytes, stream)
     _lib.call("dfs_block_score_topk", *args, p(scores), None, p(ws), need, stream)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(scores).all())
+    with_scores = col.clone()
+    col.fill_(-1)
+    _lib.call("dfs_block_score_topk", *args, None, None, p(ws), need, stream)
+    torch.cuda.synchronize()
+    assert torch.equal(col, with_scores)
 
 
 @pytest.mark.parametrize("direction", ["rising", "falling"])
