@@ -37,6 +37,18 @@ __device__ __forceinline__ uint32_t order_key(float s) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Inclusive prefix sum over the 64 lanes: shifts within rows of 16, then the
+// row totals carried by DPP row broadcasts.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return x;
+}
+
 __device__ __forceinline__ uint64_t lanes_below(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
@@ -65,12 +77,7 @@ __device__ __forceinline__ void select_row(const float* scores, int n_cand, int 
 #pragma unroll
     for (int i = 0; i < 4; ++i) c[i] = hist[255 - 4 * lane - i];
     const uint32_t own = c[0] + c[1] + c[2] + c[3];
-    uint32_t incl = own;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const uint32_t o = __shfl_up(incl, off);
-      if (lane >= off) incl += o;
-    }
+    const uint32_t incl = wave_incl_scan(own);
     const uint32_t excl = incl - own;
     const bool mine = excl < static_cast<uint32_t>(remaining) &&
                       static_cast<uint32_t>(remaining) <= incl;
@@ -81,8 +88,8 @@ __device__ __forceinline__ void select_row(const float* scores, int n_cand, int 
     }
     const uint64_t who = __ballot(mine);
     const int src = __ffsll(static_cast<unsigned long long>(who)) - 1;
-    const int digit = __shfl(255 - 4 * lane - pick, src);
-    const uint32_t above_d = __shfl(above, src);
+    const int digit = __builtin_amdgcn_readlane(255 - 4 * lane - pick, src);
+    const uint32_t above_d = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(above), src));
     prefix |= static_cast<uint32_t>(digit) << shift;
     pmask |= 255u << shift;
     remaining -= static_cast<int>(above_d);
@@ -191,6 +198,10 @@ __device__ __forceinline__ void load_q_prescaled(const ScoreParams& p, bool vali
 __device__ __forceinline__ float xhalf_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Value of lane l ^ 1 (DPP quad permutation [1, 0, 3, 2]).
+__device__ __forceinline__ float quad_swap_pairs(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
 }
 __device__ __forceinline__ float xhalf_sum(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -653,54 +664,77 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     }
   }
 
-  // One pass: the block sums of a row, sum over its TPB query tiles of
-  // (workspace sum) / Z, go to a wave-private LDS row in the key-chunk
-  // buffers (free now; ROW_CAP columns per wave) and to scores_out when the
-  // caller asked for scores; the selection reads the LDS row.
-  constexpr int ROW_CAP = TILE / 2;  // floats: each key-chunk buffer (2 x TILE uint16) holds two waves' rows
-  float* const rowbuf = reinterpret_cast<float*>(w < 2 ? &kbuf0[0][0] : &kbuf1[0][0]) + (w & 1) * ROW_CAP;
-  for (int g = 0; g < QBW; ++g) {
-    const int qb = qbw + g;
-    if (qb >= pol.Qb) break;
-    const int64_t row = static_cast<int64_t>(h) * pol.Qb + qb;
-    int32_t* cols = p.col_idx + p.row_ptr[row];
-    uint8_t* mrow = p.mask_out ? p.mask_out + row * pol.Kb : nullptr;
-    const bool dense = qb >= pol.dense_row || qb >= pol.scored_rows;
-    if constexpr (ONE_PASS) {
-      if (qb < score_rows) {
-        constexpr int WG_TILES = G * TPB;
-        float iz[TPB];
+  if constexpr (ONE_PASS) {
+    // Block sums of a row: the sum over its TPB query tiles of (workspace
+    // sum) / Z. They are formed for a group of the wave's rows at a time in
+    // wave-private LDS rows (the freed key-chunk buffers, ROW_CAP floats per
+    // wave), written to scores_out when the caller asked for scores, and the
+    // selection reads the LDS rows. The workspace is swept in whole 128-byte
+    // lines: lane l reads tiles 4 (l % 8) .. +3 of key block kb0 + l / 8, so
+    // one load instruction covers 8 key blocks of the wave's 32 tiles.
+    constexpr int ROW_CAP = TILE / 2;  // floats: each key-chunk buffer (2 x TILE uint16) holds two waves' rows
+    constexpr int WG_TILES = G * TPB;
+    float* const rowbuf = reinterpret_cast<float*>(w < 2 ? &kbuf0[0][0] : &kbuf1[0][0]) + (w & 1) * ROW_CAP;
+    const int sub = lane & 7, kq = lane >> 3;
+    const int gl = TPB == 8 ? sub >> 1 : sub;            // the row (of the wave's QBW) of this lane's tiles
+    const bool writer = TPB == 8 ? (sub & 1) == 0 : true;  // holds the row's sum after the pair exchange
+    float iz[4];
 #pragma unroll
-        for (int i = 0; i < TPB; ++i) iz[i] = inv_z[w * 32 + g * TPB + i];
-        const float* src = p.tile_sums + (static_cast<int64_t>(h) * gridDim.x + blockIdx.x) * p.tile_cols * WG_TILES +
-                           w * 32 + g * TPB;
-        float* out = p.scores_out ? p.scores_out + (static_cast<int64_t>(h) * pol.scored_rows + qb) * pol.Kb : nullptr;
-#pragma unroll 4
-        for (int kb = lane; kb < pol.Kb; kb += kWave) {
-          const float4* u = reinterpret_cast<const float4*>(src + static_cast<int64_t>(kb) * WG_TILES);
-          float t[8];
-          const float4 a = u[0];
-          t[0] = a.x * iz[0]; t[1] = a.y * iz[1]; t[2] = a.z * iz[2]; t[3] = a.w * iz[3];
-          float v;
-          if constexpr (TPB == 8) {
-            const float4 b4 = u[1];
-            t[4] = b4.x * iz[4]; t[5] = b4.y * iz[5]; t[6] = b4.z * iz[6]; t[7] = b4.w * iz[7];
-            v = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
-          } else {
-            v = (t[0] + t[1]) + (t[2] + t[3]);
+    for (int i = 0; i < 4; ++i) iz[i] = inv_z[w * 32 + 4 * sub + i];
+    const float* src = p.tile_sums + (static_cast<int64_t>(h) * gridDim.x + blockIdx.x) * p.tile_cols * WG_TILES +
+                       w * 32 + 4 * sub;
+    const int rs = max(1, min(QBW, ROW_CAP / pol.Kb));  // rows per group
+    for (int g0 = 0; g0 < QBW; g0 += rs) {
+      const int ng = min(rs, QBW - g0);
+      if (qbw + g0 < min(score_rows, pol.Qb)) {
+        const int qbl = qbw + gl;
+        const bool mine = writer && gl >= g0 && gl < g0 + ng && qbl < score_rows;
+        float* dst = rowbuf + (gl - g0) * pol.Kb;
+        float* out = p.scores_out && mine ? p.scores_out + (static_cast<int64_t>(h) * pol.scored_rows + qbl) * pol.Kb
+                                          : nullptr;
+        for (int kb0 = 0; kb0 < pol.Kb; kb0 += 64) {
+          float4 a[8];  // eight loads in flight
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int kb = kb0 + 8 * j + kq;
+            a[j] = kb < pol.Kb ? *reinterpret_cast<const float4*>(src + static_cast<int64_t>(kb) * WG_TILES)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
           }
-          rowbuf[kb] = v;
-          if (out) out[kb] = v;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int kb = kb0 + 8 * j + kq;
+            float v = (a[j].x * iz[0] + a[j].y * iz[1]) + (a[j].z * iz[2] + a[j].w * iz[3]);
+            if constexpr (TPB == 8) v += quad_swap_pairs(v);  // the row's other four tiles
+            if (mine && kb < pol.Kb) {
+              dst[kb] = v;
+              if (out) out[kb] = v;
+            }
+          }
         }
         lds_sync_wave();
       }
-      if (dense)
-        dense_row(pol.Kb, cols, mrow, lane);
-      else
-        select_row(rowbuf, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow, hist + w * 256, lane);
-      lds_sync_wave();  // the next row may overwrite rowbuf
-    } else {
-      if (dense)
+      for (int g = g0; g < g0 + ng; ++g) {
+        const int qb = qbw + g;
+        if (qb >= pol.Qb) break;
+        const int64_t row = static_cast<int64_t>(h) * pol.Qb + qb;
+        int32_t* cols = p.col_idx + p.row_ptr[row];
+        uint8_t* mrow = p.mask_out ? p.mask_out + row * pol.Kb : nullptr;
+        if (qb >= pol.dense_row || qb >= pol.scored_rows)
+          dense_row(pol.Kb, cols, mrow, lane);
+        else
+          select_row(rowbuf + (g - g0) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow,
+                     hist + w * 256, lane);
+      }
+      lds_sync_wave();  // the next group may overwrite rowbuf
+    }
+  } else {
+    for (int g = 0; g < QBW; ++g) {
+      const int qb = qbw + g;
+      if (qb >= pol.Qb) break;
+      const int64_t row = static_cast<int64_t>(h) * pol.Qb + qb;
+      int32_t* cols = p.col_idx + p.row_ptr[row];
+      uint8_t* mrow = p.mask_out ? p.mask_out + row * pol.Kb : nullptr;
+      if (qb >= pol.dense_row || qb >= pol.scored_rows)
         dense_row(pol.Kb, cols, mrow, lane);
       else
         select_row(bsum + (w * QBW + g) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow,
