@@ -9,7 +9,12 @@ the fused inverse permutation.
 
 Prints one JSON line (metric = ms per call, lower is better) with the
 roofline of the attention kernel, per-phase kernel times and a CPU baseline
-(the fp32 oracle on a bounded sample of the same inputs, scaled up).
+(the fp32 oracle on a bounded sample of the same inputs, scaled up). Two
+side measurements ride on the same line: the attention kernel on bf16
+operands (the reference kernel's operand precision) over the same mask, and
+a less local mask at the same density (K drawn from a field of its own, so a
+row's kept blocks spread over the whole row): its whole-call median and its
+attention kernel time.
 
 ``--workload cfg2`` measures the HunyuanVideo call instead (configs[2]:
 118,800 video + 256 text tokens, 24 heads), and ``--workload cfg3`` the
@@ -134,6 +139,65 @@ def run_gpu(args):
     log(f"phase times (ms): {phase_ms}")
     flops = csr_flops(row_ptr.cpu().numpy(), col_idx.cpu().numpy(), cfg.heads, L, cfg.head_dim)
     att_tflops = flops / (phase_ms["attention"] * 1e-3) / 1e12
+
+    def attention_ms(prep_x, cols):
+        """Mean HIP-event time of the attention kernel on the current stream."""
+        ops.bsa_fwd(prep_x, row_ptr, cols, out_perm=perm_d)
+        times = []
+        for _ in range(reps):
+            a, b = _events()
+            a.record()
+            ops.bsa_fwd(prep_x, row_ptr, cols, out_perm=perm_d)
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b))
+        return float(np.mean(times))
+
+    # The same mask on bf16 operands (Q, K, V and P in bf16, the reference
+    # kernel's operand precision) beside the default f16 operands.
+    del prep
+    prep16 = ops.prepare_qkv(q, k, v, perm_d, layout, operand_dtype=torch.bfloat16, pool=False)
+    bf16_ms = attention_ms(prep16, col_idx)
+    del prep16
+    log(f"attention on bf16 operands: {bf16_ms:.3f} ms")
+
+    # A less local mask at the same density: K from a field of its own, so
+    # the kept blocks of a row spread over the whole row instead of clustering
+    # near the diagonal; the whole call and the attention kernel on it.
+    qn, kn, vn = synth_qkv(cfg, device=dev, independent_keys=True)
+    call_n = []
+    for i in range(max(10, args.warmup + 5)):
+        a, b = _events()
+        a.record()
+        dfs_attention(qn, kn, vn, step_idx=0, skip_steps=0, cache_interval=1, layer_idx=1,
+                      sparsity=cfg.sparsity, sparsity_dcrt=0.0, tile_size=cfg.tile, block_size=cfg.block,
+                      video_perm=video_perm, cache_flag=True)
+        b.record()
+        call_n.append((a, b))
+    torch.cuda.synchronize()
+    call_n = sorted(a.elapsed_time(b) for a, b in call_n[args.warmup:])
+    prep_n = ops.prepare_qkv(qn, kn, vn, perm_d, layout)
+    col_n, _, _ = ops.block_score_topk(prep_n, pol, row_ptr)
+    far_ms = attention_ms(prep_n, col_n)
+    flops_n = csr_flops(row_ptr.cpu().numpy(), col_n.cpu().numpy(), cfg.heads, L, cfg.head_dim)
+    rows_of = np.repeat(np.arange(cfg.heads * pol.q_blocks) % pol.q_blocks, np.diff(row_ptr.cpu().numpy()))
+
+    def near_diag(cols):
+        """Fraction of kept blocks within 8 blocks of their row's diagonal."""
+        return float(np.mean(np.abs(cols.cpu().numpy() - rows_of) <= 8))
+
+    less_local = {
+        "inputs": "synth_qkv(independent_keys=True): K from its own smoothed field",
+        "call_ms_median": round(call_n[len(call_n) // 2], 3),
+        "attention_ms": round(far_ms, 3),
+        "attention_tflops": round(flops_n / (far_ms * 1e-3) / 1e12, 1),
+        "frac": round(flops_n / (far_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "kept_density": round(flops_n / (4.0 * cfg.head_dim * L * L * cfg.heads), 4),
+        "kept_within_8_blocks_of_diagonal": round(near_diag(col_n), 4),
+        "headline_mask_kept_within_8_blocks_of_diagonal": round(near_diag(col_idx), 4),
+    }
+    log(f"less local mask: {less_local}")
+    del prep_n, qn, kn, vn
     D = cfg.head_dim
     tensor_bytes = cfg.heads * L * D * 2
     prep_bytes = 3 * 2 * tensor_bytes  # read + write of Q, K, V (pooled outputs are ~1/16 extra)
@@ -151,6 +215,9 @@ def run_gpu(args):
         "prepare_gbs": prep_bytes / (phase_ms["prepare"] * 1e-3) / 1e9,
         "score_pooled_gflop": score_flop / 1e9,
         "density": flops / (4.0 * D * L * L * cfg.heads),
+        "attention_bf16_operands": {"ms": round(bf16_ms, 3), "tflops": round(flops / (bf16_ms * 1e-3) / 1e12, 1),
+                                    "frac": round(flops / (bf16_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
+        "less_local_mask": less_local,
         "out_shape": list(out.shape),
         "inputs": (q, k, v),
     }
@@ -483,6 +550,8 @@ def main():
         "phases_ms": {k_: round(v_, 3) for k_, v_ in res["phase_ms"].items()},
         "prepare_gbs": round(res["prepare_gbs"], 1),
         "kept_density": round(res["density"], 4),
+        "attention_bf16_operands": res["attention_bf16_operands"],
+        "less_local_mask": res["less_local_mask"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

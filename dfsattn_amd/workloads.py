@@ -83,14 +83,22 @@ def rms_norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
 
 
 def synth_qkv(cfg: DfsConfig, device="cpu", dtype: Optional[torch.dtype] = None, seed: Optional[int] = None,
-              noise_std: float = 0.5, sigma: float = 2.0):
-    """(q, k, v) as [1, H, L, D] tensors of ``dtype`` (default cfg.dtype)."""
+              noise_std: float = 0.5, sigma: float = 2.0, independent_keys: bool = False):
+    """(q, k, v) as [1, H, L, D] tensors of ``dtype`` (default cfg.dtype).
+
+    Q and K share one smoothed field, so a query block scores highest on the
+    key blocks near it in the video (a local mask, as in real video DiTs).
+    With ``independent_keys`` K gets a field of its own: block scores then
+    carry no locality and the top-k mask spreads over the whole row at the
+    same density."""
     gen = torch.Generator(device=device)
     gen.manual_seed(cfg.seed if seed is None else seed)
     dtype = dtype or cfg.dtype
     field = smoothed_field(cfg.grid, cfg.heads, cfg.head_dim, sigma, gen, device)
     shape = field.shape
     q = rms_norm(field + noise_std * torch.randn(shape, generator=gen, device=device))
+    if independent_keys:
+        field = smoothed_field(cfg.grid, cfg.heads, cfg.head_dim, sigma, gen, device)
     k = rms_norm(field + noise_std * torch.randn(shape, generator=gen, device=device))
     del field
     if cfg.text_len:
