@@ -51,6 +51,19 @@ __device__ __forceinline__ float exp2_fast(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
+// Streaming 16-byte accesses (nontemporal hint) for data a kernel reads or
+// writes exactly once: they keep it from displacing cache lines that others
+// reuse.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const uint4* p) {
+  const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ void store_stream(uint4* p, const uint4& v) {
+  const u32x4_t t = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t*>(p));
+}
+
 }  // namespace dfs
 
 #define DFS_REQUIRE(cond, ...)        \

@@ -147,41 +147,54 @@ __device__ __forceinline__ void add_chunk(float acc[8], const uint4& v, bool f16
 // execution layout and writes the tile mean as a bf16 hi/lo pair. Zero rows of
 // the scoring layout count toward the mean, as in the reference's zero-padded
 // .view(...).mean(3). Tiles past the query tiles still gather text rows of Q.
+// Block bx of nbx for (head h of H, tensor Q or K).
 template <int D>
-__global__ void __launch_bounds__(256) prep_qk_kernel(PrepParams p) {
+__device__ __forceinline__ void prep_qk_tiles(const PrepParams& p, int bx, int nbx, int h, int H, bool is_k) {
   constexpr int CPR = D / 8;        // 16-byte chunks per row
   constexpr int RPP = kWave / CPR;  // rows covered per pass
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int h = blockIdx.y;
-  const bool is_k = blockIdx.z == 1;
   const uint4* src = (is_k ? p.k : p.q) + static_cast<int64_t>(h) * p.L * CPR;
   uint4* dst = (is_k ? p.k_perm : p.q_perm) + static_cast<int64_t>(h) * p.R * CPR;
 
   // Zero-fill execution rows L..R-1 (done by the last block of each tensor/head).
-  if (blockIdx.x == gridDim.x - 1) {
+  if (bx == nbx - 1) {
     const int n = (p.R - p.L) * CPR;
     for (int i = threadIdx.x; i < n; i += blockDim.x)
-      dst[static_cast<int64_t>(p.L) * CPR + i] = make_uint4(0, 0, 0, 0);
+      store_stream(dst + static_cast<int64_t>(p.L) * CPR + i, make_uint4(0, 0, 0, 0));
   }
 
-  const int t = blockIdx.x * 4 + wave;
+  const int t = bx * 4 + wave;
   if (t >= p.k_tiles) return;
   const int c = lane % CPR;
   const int g = lane / CPR;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   bool overflow = false;
-  for (int r = g; r < p.tile; r += RPP) {
-    const int x = scoring_to_exec(t * p.tile + r, p);
-    if (x >= 0) {
-      const int s = p.perm[x];
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (s >= 0 && s < p.L) val = src[static_cast<int64_t>(s) * CPR + c];
-      dst[static_cast<int64_t>(x) * CPR + c] = p.convert ? bf16x8_to_f16x8(val, &overflow) : val;
-      add_chunk(acc, val, p.in_f16 != 0);  // tile means of the input values
+  // Rows in batches of four passes: the permutation reads of a batch, then
+  // its row reads, are all in flight before the first store.
+  constexpr int BATCH = 4;
+  for (int r0 = g; r0 < p.tile; r0 += BATCH * RPP) {
+    int xs[BATCH], ss[BATCH];
+    uint4 val[BATCH];
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      const int r = r0 + b * RPP;
+      xs[b] = r < p.tile ? scoring_to_exec(t * p.tile + r, p) : -1;
+      ss[b] = xs[b] >= 0 ? p.perm[xs[b]] : -1;
+    }
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b)
+      val[b] = ss[b] >= 0 && ss[b] < p.L ? load_stream(src + static_cast<int64_t>(ss[b]) * CPR + c)
+                                         : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      if (xs[b] < 0) continue;
+      store_stream(dst + static_cast<int64_t>(xs[b]) * CPR + c,
+                   p.convert ? bf16x8_to_f16x8(val[b], &overflow) : val[b]);
+      add_chunk(acc, val[b], p.in_f16 != 0);  // tile means of the input values
     }
   }
-  if (p.flags && overflow) atomicOr(&p.flags[(is_k ? 1 : 0) * gridDim.y + h], 1);
+  if (p.flags && overflow) atomicOr(&p.flags[(is_k ? 1 : 0) * H + h], 1);
   const int n_tiles = is_k ? p.k_tiles : p.q_tiles;
   if (!p.pool || t >= n_tiles) return;
 #pragma unroll
@@ -214,14 +227,24 @@ __device__ __forceinline__ int swap23(int s) {
 
 // One block per (128-token block, head): gathers 128 V rows (zero past L),
 // transposes them to [D][128] in 8x8 register tiles, optionally converting
-// bf16 to f16.
+// bf16 to f16, and stages the block in LDS so that the stores leave as whole
+// 256-byte rows. The staging runs in two halves (head dims d with d % 8 < 4,
+// then the rest) so a block holds 16 KB of LDS at D = 128 and the CU keeps
+// its full wave count. In LDS, 16-byte chunk kg of a staged row sits at
+// position kg ^ (dg % 16) of the row (dg = d / 8), which keeps the transposed
+// writes (16 lanes, 16 rows, one chunk column) free of bank conflicts.
+// Token block kb of head h (of H) by the NT = 16 * D / 8 threads tid of the
+// workgroup, staged through `stage` (D / 2 * 16 chunks); every thread
+// reaches the two barriers, also where kb is past the end.
 template <int D>
-__global__ void __launch_bounds__(16 * (D / 8)) prep_v_kernel(PrepParams p) {
+__device__ __forceinline__ void prep_v_block(const PrepParams& p, int kb, int h, int H, int tid, uint4* stage) {
   constexpr int CPR = D / 8;
-  const int kb = blockIdx.x;
-  const int h = blockIdx.y;
-  const int dg = threadIdx.x % CPR;   // 8 head dims: dg*8 .. dg*8+7
-  const int kg = threadIdx.x / CPR;   // 8 physical token slots: kg*8 .. kg*8+7
+  constexpr int NT = 16 * CPR;            // threads
+  constexpr int CHUNKS = kBlock / 8;      // 16-byte chunks per v_t row
+  constexpr int HALF = D / 2 * CHUNKS;    // staged chunks per half
+  const bool active = kb < p.R / kBlock;
+  const int dg = tid % CPR;   // 8 head dims: dg*8 .. dg*8+7
+  const int kg = tid / CPR;   // 8 physical token slots: kg*8 .. kg*8+7
   const uint4* src = p.v + static_cast<int64_t>(h) * p.L * CPR;
   uint4 rows[8];
 #pragma unroll
@@ -229,31 +252,58 @@ __global__ void __launch_bounds__(16 * (D / 8)) prep_v_kernel(PrepParams p) {
     const int phys = kg * 8 + i;
     const int tok = kb * kBlock + (phys & ~15) + swap23(phys & 15);
     rows[i] = make_uint4(0, 0, 0, 0);
-    if (tok < p.L) {
+    if (active && tok < p.L) {
       const int s = p.perm[tok];
-      if (s >= 0 && s < p.L) rows[i] = src[static_cast<int64_t>(s) * CPR + dg];
+      if (s >= 0 && s < p.L) rows[i] = load_stream(src + static_cast<int64_t>(s) * CPR + dg);
     }
   }
   bool overflow = false;
-  uint4* dst = p.v_t + (static_cast<int64_t>(h) * (p.R / kBlock) + kb) * D * (kBlock / 8);
+  uint4* dst = p.v_t + (static_cast<int64_t>(h) * (p.R / kBlock) + kb) * D * CHUNKS;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    uint32_t e[8];
+  for (int half = 0; half < 2; ++half) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t bits = u16_at(rows[i], j);
-      if (p.convert) {
-        const float f = bf16_bits_to_f32(bits);
-        bits = f32_to_f16_bits(f);
-        overflow |= ((bits & 0x7fffu) == 0x7c00u) && !isinf(f);  // finite -> inf
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = half * 4 + jj;
+      uint32_t e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t bits = u16_at(rows[i], j);
+        if (p.convert) {
+          const float f = bf16_bits_to_f32(bits);
+          bits = f32_to_f16_bits(f);
+          overflow |= ((bits & 0x7fffu) == 0x7c00u) && !isinf(f);  // finite -> inf
+        }
+        e[i] = bits;
       }
-      e[i] = bits;
+      stage[(dg * 4 + jj) * CHUNKS + (kg ^ (dg & 15))] =
+          make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
     }
-    const int d = dg * 8 + j;
-    dst[d * (kBlock / 8) + kg] =
-        make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+    __syncthreads();
+    if (active) {
+#pragma unroll
+      for (int c = tid; c < HALF; c += NT) {
+        const int r = c / CHUNKS, pos = c % CHUNKS;  // staged row r = dg * 4 + jj
+        const int sdg = r >> 2, d = sdg * 8 + half * 4 + (r & 3);
+        store_stream(dst + d * CHUNKS + (pos ^ (sdg & 15)), stage[c]);
+      }
+    }
+    if (half == 0) __syncthreads();  // every staged chunk is read before the second half overwrites it
   }
-  if (p.flags && overflow) atomicOr(&p.flags[2 * gridDim.y + h], 1);
+  if (p.flags && overflow) atomicOr(&p.flags[2 * H + h], 1);
+}
+
+// Q and K: one wave per (tensor, head, scoring tile), four tiles per
+// workgroup (grid: tiles / 4, heads, 2).
+template <int D>
+__global__ void __launch_bounds__(256) prep_qk_kernel(PrepParams p) {
+  prep_qk_tiles<D>(p, blockIdx.x, gridDim.x, blockIdx.y, gridDim.y, blockIdx.z == 1);
+}
+
+// V: one workgroup per (128-token block, head).
+template <int D>
+__global__ void __launch_bounds__(16 * (D / 8)) prep_v_kernel(PrepParams p) {
+  __shared__ uint4 stage[D / 2 * (kBlock / 8)];
+  prep_v_block<D>(p, blockIdx.x, blockIdx.y, gridDim.y, threadIdx.x, stage);
 }
 
 // bf16 -> f16 of eight packed values times sc (a power of two).
