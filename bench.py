@@ -124,6 +124,10 @@ def run_gpu(args):
     ev = {name: [] for name in ("prepare", "score_topk", "attention")}
     for _ in range(reps):
         a0, a1 = _events(); b1, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # Keep the GPU busy (about 1 ms) while the host enqueues the three
+        # phases, so each event pair brackets GPU work only, not the host's
+        # launch latency after the synchronisation.
+        torch.cuda._sleep(2_000_000)
         a0.record()
         prep = ops.prepare_qkv(q, k, v, perm_d, layout)
         a1.record()
@@ -139,6 +143,43 @@ def run_gpu(args):
     log(f"phase times (ms): {phase_ms}")
     flops = csr_flops(row_ptr.cpu().numpy(), col_idx.cpu().numpy(), cfg.heads, L, cfg.head_dim)
     att_tflops = flops / (phase_ms["attention"] * 1e-3) / 1e12
+    D = cfg.head_dim
+    tensor_bytes = cfg.heads * L * D * 2
+    prep_bytes = 3 * 2 * tensor_bytes  # read + write of Q, K, V (pooled outputs are ~1/16 extra)
+    score_flop = 2 * layout.q_tiles * layout.k_tiles * D * cfg.heads
+
+    del prep
+    side = {}
+    if not args.headline_only:
+        side = _side_measurements(args, cfg, dev, q, k, v, video_perm, layout, pol, perm_d, row_ptr, col_idx, flops,
+                                  reps)
+    DFS_Attention.clear_cache()
+    _dfs_attention_instances.clear()
+    return {
+        "ms_per_step": ms_per_step,
+        "median_ms": median_ms,
+        "median_calls": len(per_call),
+        "wall_ms_per_step": wall_ms,
+        "phase_ms": phase_ms,
+        "attention_flop": flops,
+        "attention_tflops": att_tflops,
+        "prepare_gbs": prep_bytes / (phase_ms["prepare"] * 1e-3) / 1e9,
+        "score_pooled_gflop": score_flop / 1e9,
+        "density": flops / (4.0 * D * L * L * cfg.heads),
+        "side": side,
+        "out_shape": list(out.shape),
+        "inputs": (q, k, v),
+    }
+
+
+def _side_measurements(args, cfg, dev, q, k, v, video_perm, layout, pol, perm_d, row_ptr, col_idx, flops, reps):
+    """The attention kernel on bf16 operands over the headline mask, and a
+    less local mask at the same density (whole call and attention kernel)."""
+    from dfsattn_amd import ops
+    from dfsattn_amd.attention_wan import dfs_attention
+    from dfsattn_amd.layout import csr_flops
+    from dfsattn_amd.workloads import synth_qkv
+    L = cfg.seq_len
 
     def attention_ms(prep_x, cols):
         """Mean HIP-event time of the attention kernel on the current stream."""
@@ -155,7 +196,6 @@ def run_gpu(args):
 
     # The same mask on bf16 operands (Q, K, V and P in bf16, the reference
     # kernel's operand precision) beside the default f16 operands.
-    del prep
     prep16 = ops.prepare_qkv(q, k, v, perm_d, layout, operand_dtype=torch.bfloat16, pool=False)
     bf16_ms = attention_ms(prep16, col_idx)
     del prep16
@@ -198,28 +238,10 @@ def run_gpu(args):
     }
     log(f"less local mask: {less_local}")
     del prep_n, qn, kn, vn
-    D = cfg.head_dim
-    tensor_bytes = cfg.heads * L * D * 2
-    prep_bytes = 3 * 2 * tensor_bytes  # read + write of Q, K, V (pooled outputs are ~1/16 extra)
-    score_flop = 2 * layout.q_tiles * layout.k_tiles * D * cfg.heads
-    DFS_Attention.clear_cache()
-    _dfs_attention_instances.clear()
     return {
-        "ms_per_step": ms_per_step,
-        "median_ms": median_ms,
-        "median_calls": len(per_call),
-        "wall_ms_per_step": wall_ms,
-        "phase_ms": phase_ms,
-        "attention_flop": flops,
-        "attention_tflops": att_tflops,
-        "prepare_gbs": prep_bytes / (phase_ms["prepare"] * 1e-3) / 1e9,
-        "score_pooled_gflop": score_flop / 1e9,
-        "density": flops / (4.0 * D * L * L * cfg.heads),
         "attention_bf16_operands": {"ms": round(bf16_ms, 3), "tflops": round(flops / (bf16_ms * 1e-3) / 1e12, 1),
                                     "frac": round(flops / (bf16_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
         "less_local_mask": less_local,
-        "out_shape": list(out.shape),
-        "inputs": (q, k, v),
     }
 
 
@@ -503,6 +525,8 @@ def main():
                     help="cfg2: valid text tokens of the 256 (the rest padding, cu_seqlens [0, valid, L])")
     ap.add_argument("--dit-phase", choices=("both", "dfs", "dense"), default="both",
                     help="cfg4: time the DFS step, the dense step or both")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="cfg1: skip the bf16-operand and less-local-mask side measurements (for profiling runs)")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = 2 if args.workload == "cfg4" else 20
@@ -550,8 +574,7 @@ def main():
         "phases_ms": {k_: round(v_, 3) for k_, v_ in res["phase_ms"].items()},
         "prepare_gbs": round(res["prepare_gbs"], 1),
         "kept_density": round(res["density"], 4),
-        "attention_bf16_operands": res["attention_bf16_operands"],
-        "less_local_mask": res["less_local_mask"],
+        **res["side"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
