@@ -675,15 +675,21 @@ __device__ __forceinline__ float operand_at(const uint16_t* base, int64_t i, boo
   return f16 ? f16_bits_to_f32(base[i]) : bf16_bits_to_f32(base[i]);
 }
 
-// The rows of a call after segment 0 of cu_seqlens, in fp32 (one wave per
-// row, keys one by one with an exact running maximum). For n_seq == 2 the
-// rows [cq1, cq2) attend keys [ck1, ck2) under the same block mask indexed
-// from each segment's own start (query block (r - cq1) / 128 selects the CSR
-// row, key block j covers keys ck1 + 128 j ..), as the reference's varlen
-// kernel treats the second sequence of its batch (attention_hyvideo.py:
-// 1054-1082, the mask repeated per sequence at :359). Rows outside every
-// query segment are zero (lse -inf). Sized for short padding segments (a few
-// hundred tokens of text padding); the work grows with rows x kept keys.
+// The rows of a call after segment 0 of cu_seqlens, in fp32. A wave takes
+// RG = 4 consecutive rows of one query block (they share the block's mask
+// row) and walks their kept key blocks 64 keys at a time: one key per lane
+// for the scores of the four rows (each K row read once), an exact running
+// maximum per row and window, then P V with each lane owning D / 64 head
+// dims of the four rows and reading the window's 64 V^T slots of its dims
+// once. For n_seq == 2 the rows [cq1, cq2) attend keys [ck1, ck2) under the
+// same block mask indexed from each segment's own start (query block
+// (r - cq1) / 128 selects the CSR row, key block j covers keys ck1 + 128 j
+// ..), as the reference's varlen kernel treats the second sequence of its
+// batch (attention_hyvideo.py:1054-1082, the mask repeated per sequence at
+// :359). Rows outside every query segment are zero (lse -inf). Windows are
+// aligned to 64 keys so that a window's V^T slots are one contiguous run of
+// a physical 128-key block; keys of a window outside the column's range are
+// masked. Sized for short padding segments (a few hundred tokens).
 template <int D>
 __global__ void __launch_bounds__(256) bsa_segment_kernel(const uint16_t* __restrict__ q,
                                                           const uint16_t* __restrict__ k,
@@ -692,10 +698,14 @@ __global__ void __launch_bounds__(256) bsa_segment_kernel(const uint16_t* __rest
                                                           const int32_t* __restrict__ col_idx,
                                                           void* __restrict__ out, const int32_t* __restrict__ out_perm,
                                                           float* __restrict__ lse, SegParams p) {
-  constexpr int DPL = D / 64;  // head dims per lane
+  constexpr int RG = 4;        // rows per wave
+  constexpr int DPL = D / 64;  // head dims per lane in P V
+  constexpr int CPR = D / 8;   // 16-byte chunks of a K row
+  __shared__ float qs[4][RG][D];   // the rows' q (times the scale), per wave
+  __shared__ float ps[4][RG][64];  // the window's P in V^T slot order, per wave
   const int h = blockIdx.y;
-  const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6), n_waves = gridDim.x * 4;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wave = blockIdx.x * 4 + w, n_waves = gridDim.x * 4;
   const int cq1 = min(max(p.cu_q[1], 0), p.L);
   const int cq2 = p.n_seq == 2 ? min(max(p.cu_q[2], cq1), p.L) : cq1;
   const int ck1 = p.n_seq == 2 ? min(max(p.cu_k[1], 0), p.L) : 0;
@@ -707,78 +717,128 @@ __global__ void __launch_bounds__(256) bsa_segment_kernel(const uint16_t* __rest
     sq = ldexpf(sq, p.exps[h] + p.exps[p.H + h]);
     sv = ldexpf(1.f, p.exps[2 * p.H + h]);
   }
+  auto wave_sync = [] {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+  };
+  auto half_to_f32 = [](uint32_t bits, bool f16) { return f16 ? f16_bits_to_f32(bits) : bf16_bits_to_f32(bits); };
   const int64_t hq = static_cast<int64_t>(h) * p.R * D;
-  for (int r = cq1 + wave; r < p.L; r += n_waves) {
-    float o[DPL];
+  const uint4* krows = reinterpret_cast<const uint4*>(k + hq);
+  for (int r0 = cq1 + RG * wave; r0 < p.L; r0 += RG * n_waves) {
+    float o[RG][DPL], m[RG], l[RG];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) o[j] = 0.f;
-    float m = -INFINITY, l = 0.f;
-    if (r < cq2 && seg_kb > 0) {
-      float qv[DPL];
+    for (int i = 0; i < RG; ++i) {
+      m[i] = -INFINITY;
+      l[i] = 0.f;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) qv[j] = operand_at(q, hq + static_cast<int64_t>(r) * D + lane * DPL + j, qk16) * sq;
-      const int64_t crow = static_cast<int64_t>(h) * p.csr_qb + ((r - cq1) >> 7);
+      for (int j = 0; j < DPL; ++j) o[i][j] = 0.f;
+    }
+    if (r0 < cq2 && seg_kb > 0) {  // RG divides 128: the group's rows share query block (r0 - cq1) / 128
+#pragma unroll
+      for (int i = 0; i < RG; ++i)
+        for (int j = lane; j < D; j += 64)
+          qs[w][i][j] = r0 + i < cq2 ? operand_at(q, hq + static_cast<int64_t>(r0 + i) * D + j, qk16) * sq : 0.f;
+      wave_sync();
+      const int64_t crow = static_cast<int64_t>(h) * p.csr_qb + ((r0 - cq1) >> 7);
       const int beg = row_ptr[crow], end = row_ptr[crow + 1];
-      for (int idx = beg; idx < end; ++idx) {
-        const int cb = col_idx[idx];
-        if (cb < 0 || cb >= seg_kb) continue;
+      for (int idx = beg; idx < end; ++idx) {  // columns ascend: stop at the segment's last block
+        const int cb = __builtin_amdgcn_readfirstlane(col_idx[idx]);
+        if (cb >= seg_kb) break;
+        if (cb < 0) continue;
         const int k0 = ck1 + cb * 128, k1 = min(k0 + 128, ck2);
-        for (int key = k0; key < k1; key += 4) {
-          float s[4];
+        for (int w0 = k0 & ~63; w0 < k1; w0 += 64) {
+          const int key = w0 + lane;
+          const bool valid = key >= k0 && key < k1;
+          // the window's V^T slots of this lane's dims, loaded with the K row
+          const int64_t vb = (static_cast<int64_t>(h) * (p.R / 128) + (w0 >> 7)) * D * 128 + (w0 & 127);
+          uint4 vv[DPL][8];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            float part = 0.f;
-            if (key + u < k1) {
+          for (int j = 0; j < DPL; ++j)
 #pragma unroll
-              for (int j = 0; j < DPL; ++j)
-                part += qv[j] * operand_at(k, hq + static_cast<int64_t>(key + u) * D + lane * DPL + j, qk16);
+            for (int c = 0; c < 8; ++c)
+              vv[j][c] = reinterpret_cast<const uint4*>(vt + vb + static_cast<int64_t>(lane * DPL + j) * 128)[c];
+          float s[RG];
+#pragma unroll
+          for (int i = 0; i < RG; ++i) s[i] = 0.f;
+          if (valid) {
+            const uint4* kr = krows + static_cast<int64_t>(key) * CPR;
+#pragma unroll 2
+            for (int c = 0; c < CPR; ++c) {
+              asm volatile("" ::: "memory");  // q stays in LDS (read per chunk), not hoisted into registers
+              const uint4 kv = kr[c];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float kf = half_to_f32(u16_at(kv, e), qk16);
+#pragma unroll
+                for (int i = 0; i < RG; ++i) s[i] += qs[w][i][c * 8 + e] * kf;
+              }
             }
-            s[u] = part;
           }
+          // slot of window key `lane` in its 16-key group: swap23 (an involution)
+          const int slot = (lane & ~15) | (lane & 3) | ((lane & 4) << 1) | ((lane & 8) >> 1);
 #pragma unroll
-          for (int off = 32; off >= 1; off >>= 1)
+          for (int i = 0; i < RG; ++i) {
+            const float si = valid ? s[i] : -INFINITY;
+            float mx = si;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) s[u] += __shfl_xor(s[u], off, 64);
-          float mx = m;
+            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            const float mnew = fmaxf(m[i], mx);  // finite: the window holds key max(w0, k0) < k1
+            const float alpha = exp2_fast(m[i] - mnew);
+            const float pk = valid ? exp2_fast(si - mnew) : 0.f;
+            float psum = pk;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if (key + u >= k1) s[u] = -INFINITY;
-            mx = fmaxf(mx, s[u]);
+            for (int off = 32; off >= 1; off >>= 1) psum += __shfl_xor(psum, off, 64);
+            l[i] = l[i] * alpha + psum;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) o[i][j] *= alpha;
+            m[i] = mnew;
+            ps[w][i][slot] = pk;
           }
-          const float alpha = exp2_fast(m - mx);
-          l *= alpha;
+          wave_sync();
+#pragma unroll 1
+          for (int c = 0; c < 8; ++c) {
+            asm volatile("" ::: "memory");  // P of 8 slots read per step, not all at once
+            float pc[RG][8];
 #pragma unroll
-          for (int j = 0; j < DPL; ++j) o[j] *= alpha;
+            for (int i = 0; i < RG; ++i)
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if (key + u >= k1) continue;
-            const float pu = exp2_fast(s[u] - mx);
-            l += pu;
-            const int t = key + u, tb = t & 127;
-            const int slot = (tb & ~15) | ((tb & 3) | ((tb & 4) << 1) | ((tb & 8) >> 1));  // swap23 (an involution)
-            const int64_t vb = (static_cast<int64_t>(h) * (p.R / 128) + (t >> 7)) * D * 128;
+              for (int e = 0; e < 8; ++e) pc[i][e] = ps[w][i][c * 8 + e];
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) o[j] += pu * operand_at(vt, vb + static_cast<int64_t>(lane * DPL + j) * 128 + slot, pv16);
+            for (int j = 0; j < DPL; ++j) {
+              const uint4 vc = c == 0 ? vv[j][0] : c == 1 ? vv[j][1] : c == 2 ? vv[j][2] : c == 3 ? vv[j][3]
+                             : c == 4 ? vv[j][4] : c == 5 ? vv[j][5] : c == 6 ? vv[j][6] : vv[j][7];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float vf = half_to_f32(u16_at(vc, e), pv16);
+#pragma unroll
+                for (int i = 0; i < RG; ++i) o[i][j] += pc[i][e] * vf;
+              }
+            }
           }
-          m = mx;
+          wave_sync();  // ps is read before the next window overwrites it
         }
       }
     }
-    const float inv = l > 0.f ? sv / l : 0.f;
-    const int orow = out_perm ? out_perm[r] : r;
-    const int64_t ob = (static_cast<int64_t>(h) * p.Lo + orow) * D + lane * DPL;
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const float v = o[j] * inv;
-      if (p.out_kind == DFS_DTYPE_F32)
-        static_cast<float*>(out)[ob + j] = v;
-      else if (p.out_kind == DFS_DTYPE_BF16)
-        static_cast<uint16_t*>(out)[ob + j] = static_cast<uint16_t>(f32_to_bf16_bits(v));
-      else
-        static_cast<uint16_t*>(out)[ob + j] = static_cast<uint16_t>(f32_to_f16_bits(v));
+    for (int i = 0; i < RG; ++i) {
+      const int r = r0 + i;
+      if (r >= p.L) break;
+      const float inv = l[i] > 0.f ? sv / l[i] : 0.f;
+      const int orow = out_perm ? out_perm[r] : r;
+      const int64_t ob = (static_cast<int64_t>(h) * p.Lo + orow) * D + lane * DPL;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const float v = o[i][j] * inv;
+        if (p.out_kind == DFS_DTYPE_F32)
+          static_cast<float*>(out)[ob + j] = v;
+        else if (p.out_kind == DFS_DTYPE_BF16)
+          static_cast<uint16_t*>(out)[ob + j] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+        else
+          static_cast<uint16_t*>(out)[ob + j] = static_cast<uint16_t>(f32_to_f16_bits(v));
+      }
+      if (lse && lane == 0)
+        lse[static_cast<int64_t>(h) * p.Lo + r] = l[i] > 0.f ? (m[i] + log2f(l[i])) * 0.69314718055994531f : -INFINITY;
     }
-    if (lse && lane == 0)
-      lse[static_cast<int64_t>(h) * p.Lo + r] = l > 0.f ? (m + log2f(l)) * 0.69314718055994531f : -INFINITY;
   }
 }
 
