@@ -27,6 +27,10 @@ each prints its own JSON line. The default run (cfg1) is the benchmark line.
 Wan-style DiT with DFS self-attention against the same step with
 dense self-attention.
 
+The line's ``dtype`` is the MFMA operand type of the DFS kernels (f16: the
+bf16 inputs are rounded to f16, a head beyond the f16 range is stored scaled
+by a power of two) and ``input_dtype`` the type of the tensors passed in.
+
 ``--copy-calibration`` instead runs one plain 1 GiB device copy (torch's copy
 kernel), the known-size reference the FETCH_SIZE / WRITE_SIZE counters of the
 attention kernel are scaled by. The per-launch HBM traffic those counter runs
@@ -295,7 +299,7 @@ def run_cfg2(args):
     return {"metric": "DFS attn ms/call @119,056 tok (118,800 video + 256 text),24h,d128 bf16",
             "value": round(ms, 3), "unit": "ms/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-            "dtype": "bf16", "data": "synthetic (smoothed-field Q/K, iid V, iid text; seeded)",
+            "dtype": "f16", "input_dtype": "bf16", "data": "synthetic (smoothed-field Q/K, iid V, iid text; seeded)",
             "config": {"workload": "cfg2 HunyuanVideo joint attention: 33x45x80 video + 256 text tokens, 24 heads, "
                                    "d128, tile 16, block 128, hilbert3d, sparsity 0.3, fresh mask per call" + pad,
                        "global_batch": 1, "seq_len": cfg.seq_len, "parallelism": "none (1 GPU)"},
@@ -376,7 +380,7 @@ def run_cfg3(args):
     return {"metric": "DFS mask-cache regime amortized ms/step @75.6k tok,40h,d128 bf16 (50 steps)",
             "value": base["amortized_ms_per_step"], "unit": "ms/step", "n_gpus": 1, "steps": steps, "warmup": 0,
             "ms_per_step": base["amortized_ms_per_step"], "higher_is_better": False, "scaling": "weak",
-            "vs_baseline": None, "dtype": "bf16",
+            "vs_baseline": None, "dtype": "f16", "input_dtype": "bf16",
             "data": "synthetic cfg1 inputs, Q/K drift N(0,0.02) per step (seeded)",
             "config": {"workload": "cfg3 mask-cache regime: 50 calls, skip_steps 12 (dense), cache_interval 12, "
                                    "value = sparsity 0.3, sparsity_dcrt 0", "global_batch": 1, "seq_len": L,
@@ -436,7 +440,7 @@ def run_cfg4(args):
     return {"metric": "DiT denoising step ms (40 blocks, 75.6k tok, d5120, CFG) with DFS self-attention s=0.3",
             "value": round(sparse_ms, 1), "unit": "ms/step", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(sparse_ms, 1), "higher_is_better": False,
-            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "attention_dtype": "f16",
             "data": "synthetic (random-init N(0, 0.02) bf16 weights, N(0, 1) latent and text context; seeded)",
             "config": {"workload": "cfg4 Wan-style DiT step: 40 blocks, hidden 5120, 40 heads, FFN 13824, "
                                    "QK-RMSNorm + 3D RoPE, 512x4096 text context, latent 21x45x80 tokens, "
@@ -568,7 +572,8 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "f16",
+        "input_dtype": "bf16",
         "data": "synthetic (smoothed-field Q/K, iid V; seeded)",
         "config": {"workload": "cfg1 Wan single DFS call: B=1, 21x45x80=75600 tokens, 40 heads, d128, "
                                "tile 16, block 128, hilbert3d, sparsity 0.3, fresh mask per call",

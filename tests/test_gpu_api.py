@@ -15,6 +15,43 @@ def _rel(out, ref):
     return float((out.double() - ref.double()).abs().mean() / ref.double().abs().mean())
 
 
+def _assert_selection(mask, q, k, v, perm, sparsity, tile, ref_scores, dev, video_len=None):
+    """The cached mask is the oracle's selection rule applied to the GPU's own
+    fp32 block scores, bit-exact; and every row where it differs from the
+    selection over the oracle's fp32 scores is one whose k-th and (k+1)-th
+    oracle candidate scores lie closer than twice the measured score error
+    (two scores each off by at most that much can swap)."""
+    from dfsattn_amd import ops
+    from dfsattn_amd.layout import ScoringLayout, hunyuan_policy, wan_policy
+
+    L, H = q.shape[2], q.shape[1]
+    full, _ = orc.full_permutation(perm, L)
+    lay = ScoringLayout(L, video_len or L, tile)
+    pol = hunyuan_policy(lay, sparsity) if video_len else wan_policy(lay, sparsity)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ops.device_perm(full, dev), lay)
+    row_ptr = torch.from_numpy(pol.row_ptr(H)).to(dev)
+    _, scores, _ = ops.block_score_topk(prep, pol, row_ptr, want_scores=True)
+    got = scores.cpu()
+
+    def pick(s):
+        return (orc.mask_from_scores_hunyuan(s, sparsity, L, video_len) if video_len
+                else orc.mask_from_scores_wan(s, sparsity))
+
+    assert torch.equal(mask, pick(got))
+    ref_sel = pick(ref_scores)
+    err = float((got - ref_scores).abs().max())
+    differ = [(h, r) for h in range(H) for r in range(ref_scores.shape[1]) if not torch.equal(mask[h, r], ref_sel[h, r])]
+    gaps = []
+    for h, r in differ:
+        assert pol.k_pick < pol.n_cand, (h, r)  # every candidate kept: nothing can swap
+        top = torch.sort(ref_scores[h, r, :pol.n_cand], descending=True).values
+        gaps.append(float(top[pol.k_pick - 1] - top[pol.k_pick]))
+    print(f"{len(differ)} of {H * ref_scores.shape[1]} rows select differently from the oracle's fp32 scores; "
+          f"max score error {err:.2e}, largest k-th/(k+1)-th gap among them {max(gaps, default=0.0):.2e}",
+          flush=True)
+    assert all(g <= 2 * err for g in gaps), (gaps, err)
+
+
 @pytest.fixture(autouse=True)
 def _clean():
     from dfsattn_amd import attention_hyvideo as hy
@@ -43,7 +80,7 @@ def test_wan_cfg0_shape_matches_oracle(dev):
     entry = DFS_Attention._cached_metadata[(3, "native", 128, 16, 16)]
     mask = entry["block_mask"].cpu()
     assert mask.shape == ref_mask.shape
-    assert (mask == ref_mask).float().mean() > 0.99
+    _assert_selection(mask, q, k, v, perm, 0.3, 16, ref_scores, dev)
     # output against the oracle attention on the GPU's own mask (fp32 reference)
     p, inv = orc.full_permutation(perm, q.shape[2])
     ref_own = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
@@ -93,11 +130,12 @@ def test_hunyuan_with_text_matches_oracle(dev):
     out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=12, skip_steps=12, cache_interval=12,
                         layer_idx=0, sparsity=0.5, sparsity_dcrt=0.1, tile_size=16, video_len=vl,
                         video_perm=perm)
-    ref, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.5, 16, video_len=vl)
+    ref, ref_mask, ref_scores = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.5, 16,
+                                                            video_len=vl)
     key = next(iter(DFS_Attention._cached_metadata))
     mask = DFS_Attention._cached_metadata[key]["block_mask"].cpu()
     assert mask[:, :, vl // 128:].all() and mask[:, vl // 128:].all()
-    assert (mask == ref_mask).float().mean() > 0.99
+    _assert_selection(mask, q, k, v, perm, 0.5, 16, ref_scores, dev, video_len=vl)
     p, inv = orc.full_permutation(perm, L)
     ref_own = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
     assert _rel(out.cpu(), ref_own) < 4e-3
@@ -164,9 +202,9 @@ def test_hunyuan_padding_segment_matches_oracle(dev, grid, text_len, pad, via):
                         video_perm=perm, max_seqlen_q=valid, max_seqlen_kv=valid, **kw)
     key = next(iter(DFS_Attention._cached_metadata))
     mask = DFS_Attention._cached_metadata[key]["block_mask"].cpu()
-    _, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.5, 16, video_len=vl,
-                                                 valid=valid)
-    assert (mask == ref_mask).float().mean() > 0.99
+    _, _, ref_scores = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.5, 16, video_len=vl,
+                                                   valid=valid)
+    _assert_selection(mask, q, k, v, perm, 0.5, 16, ref_scores, dev, video_len=vl)
     p, inv = orc.full_permutation(perm, L)
     ref = orc.segment_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask, [0, valid, L])
     ref = ref[:, :, inv]
@@ -195,9 +233,9 @@ def test_wan_other_token_orders_match_oracle(dev, order):
     out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), step_idx=24, skip_steps=12, cache_interval=12,
                         layer_idx=0, sparsity=0.3, sparsity_dcrt=0.1, tile_size=16, video_perm=perm)
     ref_perm = torch.arange(cfg.seq_len) if perm is None else perm
-    _, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), ref_perm, 0.3, 16)
+    _, _, ref_scores = orc.dfs_attention_reference(q.float(), k.float(), v.float(), ref_perm, 0.3, 16)
     mask = DFS_Attention._cached_metadata[(0, "native", 128, 16, 16)]["block_mask"].cpu()
-    assert (mask == ref_mask).float().mean() > 0.99
+    _assert_selection(mask, q, k, v, ref_perm, 0.3, 16, ref_scores, dev)
     p, inv = orc.full_permutation(ref_perm, cfg.seq_len)
     ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
     assert _rel(out.cpu(), ref) < 4e-3
@@ -259,8 +297,8 @@ def test_default_path_keeps_inputs_beyond_f16(dev):
                         layer_idx=5, sparsity=0.3, sparsity_dcrt=0.1, tile_size=16, video_perm=perm)
     assert bool(torch.isfinite(out).all())
     mask = DFS_Attention._cached_metadata[(5, "native", 128, 16, 16)]["block_mask"].cpu()
-    _, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.3, 16)
-    assert (mask == ref_mask).float().mean() > 0.97
+    _, _, ref_scores = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.3, 16)
+    _assert_selection(mask, q, k, v, perm, 0.3, 16, ref_scores, dev)
     p, inv = orc.full_permutation(perm, q.shape[2])
     ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
     for h in range(4):
@@ -338,8 +376,8 @@ def test_wan_edge_shapes_match_oracle(dev, grid, heads, d, dtype, sparsity):
                         layer_idx=7, sparsity=sparsity, sparsity_dcrt=0.0, tile_size=16, video_perm=perm)
     assert out.shape == q.shape and out.dtype == dtype
     mask = DFS_Attention._cached_metadata[(7, "native", 128, 16, 16)]["block_mask"].cpu()
-    _, ref_mask, _ = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, sparsity, 16)
-    assert (mask == ref_mask).float().mean() > 0.95
+    _, _, ref_scores = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, sparsity, 16)
+    _assert_selection(mask, q, k, v, perm, sparsity, 16, ref_scores, dev)
     kb = mask.shape[-1]
     assert bool((mask.sum(-1) == max(1, int(sparsity * kb))).all())
     p, inv = orc.full_permutation(perm, q.shape[2])
