@@ -55,27 +55,40 @@ __device__ __forceinline__ uint64_t lanes_below(int lane) {
 
 // Selection of one mask row by one wave.
 //  * columns [0, n_cand): the k_pick largest scores, ties broken by lower
-//    column first (radix select on the order keys, 4 x 8-bit digits);
+//    column first (radix select on the order keys, up to 4 x 8-bit digits);
 //  * columns [n_cand, dense_col): never kept;
 //  * columns [dense_col, kb): always kept.
 // cols receives the kept columns in ascending order; mask_row (optional) the
-// uint8 mask. hist is 256 words of wave-private LDS.
+// uint8 mask. hist is 256 * NSUB words of wave-private LDS: NSUB copies of the
+// digit histogram, interleaved per digit, with lane l counting into copy
+// l % NSUB, so lanes whose keys share a digit split over NSUB addresses (the
+// leading digits of block scores take few values, and the LDS serialises
+// atomics on one address). The digits stop early once every key sharing the
+// k-th key's leading digits is kept: the set is then fixed without resolving
+// the remaining bits.
+template <int NSUB = 1>
 __device__ __forceinline__ void select_row(const float* scores, int n_cand, int k_pick, int dense_col, int kb,
-                           int32_t* cols, uint8_t* mask_row, uint32_t* hist, int lane) {
+                                           int32_t* cols, uint8_t* mask_row, uint32_t* hist, int lane) {
+  static_assert(NSUB == 1 || NSUB == 2 || NSUB == 4, "sub-histograms per digit");
   uint32_t prefix = 0, pmask = 0;
   int remaining = k_pick;
+  const uint32_t copy = static_cast<uint32_t>(lane) & (NSUB - 1);
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = lane; b < 256; b += kWave) hist[b] = 0;
+    for (int b = lane; b < 256 * NSUB; b += kWave) hist[b] = 0;
     lds_sync_wave();
     for (int j = lane; j < n_cand; j += kWave) {
       const uint32_t key = order_key(scores[j]);
-      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      if ((key & pmask) == prefix) atomicAdd(&hist[((key >> shift) & 255u) * NSUB + copy], 1u);
     }
     lds_sync_wave();
     // Lane i owns digits 255-4i .. 252-4i, highest first.
     uint32_t c[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = hist[255 - 4 * lane - i];
+    for (int i = 0; i < 4; ++i) {
+      c[i] = 0;
+#pragma unroll
+      for (int k = 0; k < NSUB; ++k) c[i] += hist[(255 - 4 * lane - i) * NSUB + k];
+    }
     const uint32_t own = c[0] + c[1] + c[2] + c[3];
     const uint32_t incl = wave_incl_scan(own);
     const uint32_t excl = incl - own;
@@ -88,20 +101,24 @@ __device__ __forceinline__ void select_row(const float* scores, int n_cand, int 
     }
     const uint64_t who = __ballot(mine);
     const int src = __ffsll(static_cast<unsigned long long>(who)) - 1;
+    const uint32_t in_bin = mine ? c[pick] : 0u;
     const int digit = __builtin_amdgcn_readlane(255 - 4 * lane - pick, src);
     const uint32_t above_d = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(above), src));
+    const uint32_t bin = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(in_bin), src));
     prefix |= static_cast<uint32_t>(digit) << shift;
     pmask |= 255u << shift;
     remaining -= static_cast<int>(above_d);
+    if (bin == static_cast<uint32_t>(remaining)) break;  // the whole bin is kept
   }
-  // prefix is the order key of the k-th largest score; `remaining` of the
-  // candidates equal to it are kept, lowest column first.
+  // The k-th largest key agrees with prefix on the bits of pmask; every key
+  // above that is kept, and `remaining` of the keys equal to it there, lowest
+  // column first.
   const uint64_t below = lanes_below(lane);
   int out = 0, ties = 0;
   for (int base = 0; base < n_cand; base += kWave) {
     const int j = base + lane;
     const bool valid = j < n_cand;
-    const uint32_t key = valid ? order_key(scores[j]) : 0u;
+    const uint32_t key = valid ? order_key(scores[j]) & pmask : 0u;
     const bool eq = valid && key == prefix;
     const uint64_t eqb = __ballot(eq);
     const bool take = (valid && key > prefix) ||
@@ -375,7 +392,9 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
   float* bsum = GB ? (p.scores_out ? p.scores_out + (static_cast<int64_t>(h) * pol.scored_rows + qb0) * pol.Kb
                                    : nullptr)
                    : smem;
-  uint32_t* hist = reinterpret_cast<uint32_t*>(GB ? smem : smem + G * pol.Kb);  // [4][256]
+  // [4 waves][256 digits][SEL_SUB copies] of the top-k histograms
+  constexpr int SEL_SUB = GB ? 4 : 1;
+  uint32_t* hist = reinterpret_cast<uint32_t*>(GB ? smem : smem + G * pol.Kb);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
   const int score_rows = p.scores_out ? pol.scored_rows : min(pol.scored_rows, pol.dense_row);
   const int qbw = qb0 + w * QBW;  // first query block of this wave
@@ -476,9 +495,9 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       auto st_col = [&](int c, int j) { return TPB == 8 ? c * 4 + 2 * hl + j : c * 8 + 2 * j + hl; };
       float m = -INFINITY, z = 0.f;
       float pend[NST];  // this lane's sums of the previous chunk, stored one step late
-      // A chunk's sums are stored after the next chunk's barrier and copy
-      // issue, so the wait for that copy at the top of a step does not also
-      // wait for stores issued just before it.
+      // A chunk's sums are stored one step late, after the next chunk's
+      // barrier, copy issue and operand reads, so the wait for that copy at
+      // the top of a step does not also wait for stores issued just before it.
       auto flush = [&](int c) {
 #pragma unroll
         for (int j = 0; j < NST; ++j) U(st_col(c, j)) = pend[j];
@@ -488,9 +507,11 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
         block_barrier();
         issue(c + 1, std::integral_constant<int, 1 - decltype(buf)::value>{});
         if (!wave_scores) return;
-        if (c > 0) flush(c - 1);
-        __builtin_amdgcn_sched_barrier(0);  // the stores stay ahead of this chunk's MFMAs
         const f32x16 acc = chunk_scores(buf);  // s' (log2 units)
+        // The previous chunk's sums go out after this chunk's operand reads:
+        // issued before them, the stores made the compiler wait for part of
+        // the next chunk's copy ahead of the reads in every other step.
+        if (c > 0) flush(c - 1);
         const int lim = (c + 1) * ROWS <= p.k_tiles ? ROWS : p.k_tiles - c * ROWS;  // valid key tiles
         auto joint_max = [&]() {
           float cm = -INFINITY;
@@ -684,11 +705,16 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     const float* src = p.tile_sums + (static_cast<int64_t>(h) * gridDim.x + blockIdx.x) * p.tile_cols * WG_TILES +
                        w * 32 + 4 * sub;
     const int rs = max(1, min(QBW, ROW_CAP / pol.Kb));  // rows per group
+    int row_beg[QBW];  // CSR starts of the wave's rows, loaded ahead of the sweep
+#pragma unroll
+    for (int g = 0; g < QBW; ++g)
+      row_beg[g] = qbw + g < pol.Qb ? p.row_ptr[static_cast<int64_t>(h) * pol.Qb + qbw + g] : 0;
     for (int g0 = 0; g0 < QBW; g0 += rs) {
       const int ng = min(rs, QBW - g0);
       if (qbw + g0 < min(score_rows, pol.Qb)) {
         const int qbl = qbw + gl;
-        const bool mine = writer && gl >= g0 && gl < g0 + ng && qbl < score_rows;
+        const bool need = gl >= g0 && gl < g0 + ng;  // this lane's tiles belong to a row of the group
+        const bool mine = writer && need && qbl < score_rows;
         float* dst = rowbuf + (gl - g0) * pol.Kb;
         float* out = p.scores_out && mine ? p.scores_out + (static_cast<int64_t>(h) * pol.scored_rows + qbl) * pol.Kb
                                           : nullptr;
@@ -697,8 +723,9 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const int kb = kb0 + 8 * j + kq;
-            a[j] = kb < pol.Kb ? *reinterpret_cast<const float4*>(src + static_cast<int64_t>(kb) * WG_TILES)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            a[j] = need && kb < pol.Kb
+                       ? *reinterpret_cast<const float4*>(src + static_cast<int64_t>(kb) * WG_TILES)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
           }
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
@@ -717,13 +744,13 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
         const int qb = qbw + g;
         if (qb >= pol.Qb) break;
         const int64_t row = static_cast<int64_t>(h) * pol.Qb + qb;
-        int32_t* cols = p.col_idx + p.row_ptr[row];
+        int32_t* cols = p.col_idx + row_beg[g];
         uint8_t* mrow = p.mask_out ? p.mask_out + row * pol.Kb : nullptr;
         if (qb >= pol.dense_row || qb >= pol.scored_rows)
           dense_row(pol.Kb, cols, mrow, lane);
         else
-          select_row(rowbuf + (g - g0) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow,
-                     hist + w * 256, lane);
+          select_row<SEL_SUB>(rowbuf + (g - g0) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols,
+                              mrow, hist + w * 256 * SEL_SUB, lane);
       }
       lds_sync_wave();  // the next group may overwrite rowbuf
     }
@@ -737,8 +764,8 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       if (qb >= pol.dense_row || qb >= pol.scored_rows)
         dense_row(pol.Kb, cols, mrow, lane);
       else
-        select_row(bsum + (w * QBW + g) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols, mrow,
-                   hist + w * 256, lane);
+        select_row<SEL_SUB>(bsum + (w * QBW + g) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols,
+                            mrow, hist + w * 256 * SEL_SUB, lane);
     }
   }
 }
@@ -851,7 +878,7 @@ int score_topk_impl(const char* name, const uint16_t* q_pool_hi, const uint16_t*
   const size_t static_wide = 2 * 2 * 32 * static_cast<size_t>(head_dim) * 2;
   const bool wide = smem_wide + static_wide <= 160 * 1024;
   const bool global_sums = scores_out != nullptr;  // block sums kept in scores_out, not LDS
-  const size_t smem_gb = 4 * 256 * 4;
+  const size_t smem_gb = 4 * 256 * 4 * 4;  // four waves' histograms, four copies per digit
   ScoreParams p{};
   p.q_hi = reinterpret_cast<const uint4*>(q_pool_hi);
   p.q_lo = reinterpret_cast<const uint4*>(q_pool_lo);
