@@ -31,6 +31,9 @@ The line's ``dtype`` is the MFMA operand type of the DFS kernels (f16: the
 bf16 inputs are rounded to f16, a head beyond the f16 range is stored scaled
 by a power of two) and ``input_dtype`` the type of the tensors passed in.
 
+``--gemm-calibration`` instead times torch.matmul (hipBLASLt) at 16384^3 in
+bf16 and f16: the rate a vendor MFMA-bound kernel sustains on the same box.
+
 ``--copy-calibration`` instead runs one plain 1 GiB device copy (torch's copy
 kernel), the known-size reference the FETCH_SIZE / WRITE_SIZE counters of the
 attention kernel are scaled by. The per-launch HBM traffic those counter runs
@@ -516,6 +519,34 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": n * 4}), flush=True)
 
 
+def gemm_calibration():
+    """The sustained rate of the vendor's dense GEMM (torch.matmul, which
+    runs hipBLASLt) at 16384^3 in bf16 and f16: what an MFMA-bound library
+    kernel reaches on this box, next to which the attention kernel's
+    fraction of the 2.5 PFLOP/s peak is read."""
+    dev = torch.device("cuda:0")
+    n = 16384
+    res = {}
+    for name, dt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+        a = torch.randn(n, n, device=dev, dtype=dt)
+        b = torch.randn(n, n, device=dev, dtype=dt)
+        c = torch.empty(n, n, device=dev, dtype=dt)
+        for _ in range(3):
+            torch.matmul(a, b, out=c)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            torch.matmul(a, b, out=c)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 10
+        res[name] = {"ms": round(ms, 3), "tflops": round(2 * n ** 3 / ms / 1e9, 1),
+                     "frac_of_peak": round(2 * n ** 3 / ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
+        del a, b, c
+    print(json.dumps({"gemm_calibration": res, "shape": [n, n, n]}), flush=True)
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -533,6 +564,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 5; 1 for cfg4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--gemm-calibration", action="store_true")
     ap.add_argument("--workload", choices=("cfg1", "cfg2", "cfg3", "cfg4"), default="cfg1")
     ap.add_argument("--text-valid", type=int, default=None,
                     help="cfg2: valid text tokens of the 256 (the rest padding, cu_seqlens [0, valid, L])")
@@ -551,6 +583,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.gemm_calibration:
+        gemm_calibration()
         return
     if args.workload != "cfg1":
         line = {"cfg2": run_cfg2, "cfg3": run_cfg3, "cfg4": run_cfg4}[args.workload](args)
