@@ -13,8 +13,9 @@ Each function restates the reference (``codesiena/DFSattn``) at the cited
   numpy-hilbert-curve>=1.0.0 ``encode``, requirements.txt:19): pinned by
   closed forms (1 bit per axis = inverse Gray code of the interleaved
   coordinate bits, axis 0 most significant), the Hilbert-curve invariants
-  (bijection, unit steps on full 2^b cubes, index 0 at the origin) and an
-  independent C implementation. The exact numpy-hilbert-curve bit convention
+  (bijection, unit steps on full 2^b cubes, index 0 at the origin), the
+  package's published usage example (2-D, 3 bits) and an independent C
+  implementation. The exact numpy-hilbert-curve bit convention
   beyond these is **parity unpinned** (the package is absent offline and the
   reference ships no fixture for it).
 * ``compute_cache_schedule`` (dfsattn/attention_wan.py:41-66): pinned by the

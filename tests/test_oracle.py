@@ -44,6 +44,17 @@ def test_hilbert_one_bit_is_inverse_gray_of_interleaved_bits():
     assert [int(c) for c in orc.hilbert_encode(np.array([[0, 0], [0, 1], [1, 1], [1, 0]]), 2, 1)] == [0, 1, 2, 3]
 
 
+def test_hilbert_matches_the_packages_published_example():
+    # numpy-hilbert-curve's own usage example (its README, version 1.0.x):
+    # decode([1, 2, 3], 2, 3) gives [[0, 1], [1, 1], [1, 0]], and encode of
+    # those points gives [1, 2, 3]. This fixes which axis the finest level
+    # steps along first at three levels (the axes swapped give [3, 2, 1]); it
+    # does not tell the per-level exchange rule apart from leaving it out,
+    # which agree on these first points.
+    assert orc.hilbert_encode(np.array([[0, 1], [1, 1], [1, 0]]), 2, 3).tolist() == [1, 2, 3]
+    assert int(orc.hilbert_encode(np.array([0, 0]), 2, 3)) == 0
+
+
 @pytest.mark.parametrize("dims,bits", [(2, 3), (3, 2), (3, 3)])
 def test_hilbert_curve_invariants_on_full_cubes(dims, bits):
     side = 1 << bits
