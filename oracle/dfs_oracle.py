@@ -14,8 +14,10 @@ Each function restates the reference (``codesiena/DFSattn``) at the cited
   closed forms (1 bit per axis = inverse Gray code of the interleaved
   coordinate bits, axis 0 most significant), the Hilbert-curve invariants
   (bijection, unit steps on full 2^b cubes, index 0 at the origin), the
-  package's published usage example (2-D, 3 bits) and an independent C
-  implementation. The exact numpy-hilbert-curve bit convention
+  package's published usage example (2-D, 3 bits), a round trip through a
+  separate restatement of the package's ``decode`` (which fails for the
+  encoder's loops in another order or without the exchange step) and an
+  independent C implementation. The exact numpy-hilbert-curve bit convention
   beyond these is **parity unpinned** (the package is absent offline and the
   reference ships no fixture for it).
 * ``compute_cache_schedule`` (dfsattn/attention_wan.py:41-66): pinned by the
@@ -94,6 +96,37 @@ def hilbert_encode(locs: np.ndarray, num_dims: int, num_bits: int) -> np.ndarray
     weights = (np.uint64(1) << np.arange(inter.shape[1] - 1, -1, -1, dtype=np.uint64))
     codes = (binary.astype(np.uint64) * weights[None, :]).sum(axis=1, dtype=np.uint64)
     return codes.reshape(locs.shape[:-1])
+
+
+def hilbert_decode(codes: np.ndarray, num_dims: int, num_bits: int) -> np.ndarray:
+    """Integer points of Hilbert integers: numpy-hilbert-curve's ``decode``,
+    restated separately from ``hilbert_encode`` in the package's own steps:
+    the index bits (most significant first) Gray-encoded, split level by level
+    with axis 0 first, then for each bit level (least significant first) and
+    each axis (last first) the same invert/exchange of the lower bits of
+    axis 0. Kept as the second half of a round trip that pins the encoder's
+    loop orders and axis order (an exchange rule applied in another order, or
+    left out, does not invert)."""
+    codes = np.asarray(codes, dtype=np.uint64)
+    flat = codes.reshape(-1)
+    nb = num_dims * num_bits
+    if nb > 63:
+        raise ValueError("num_dims * num_bits must not exceed 63")
+    shifts = np.arange(nb - 1, -1, -1, dtype=np.uint64)
+    hbits = ((flat[:, None] >> shifts[None, :]) & np.uint64(1)).astype(bool)
+    gray = hbits.copy()
+    gray[:, 1:] ^= hbits[:, :-1]
+    gray = np.swapaxes(gray.reshape(-1, num_bits, num_dims), 1, 2).copy()
+    for bit in range(num_bits - 1, -1, -1):
+        for dim in range(num_dims - 1, -1, -1):
+            mask = gray[:, dim, bit][:, None]
+            gray[:, 0, bit + 1:] ^= mask
+            to_flip = (~mask) & (gray[:, 0, bit + 1:] ^ gray[:, dim, bit + 1:])
+            gray[:, dim, bit + 1:] ^= to_flip
+            gray[:, 0, bit + 1:] ^= to_flip
+    weights = (np.int64(1) << np.arange(num_bits - 1, -1, -1, dtype=np.int64))
+    locs = (gray.astype(np.int64) * weights[None, None, :]).sum(axis=-1)
+    return locs.reshape(codes.shape + (num_dims,))
 
 
 def hilbert3d_perm(f: int, h: int, w: int) -> np.ndarray:

@@ -55,6 +55,26 @@ def test_hilbert_matches_the_packages_published_example():
     assert int(orc.hilbert_encode(np.array([0, 0]), 2, 3)) == 0
 
 
+def test_hilbert_decode_matches_the_packages_published_example():
+    assert orc.hilbert_decode(np.array([1, 2, 3]), 2, 3).tolist() == [[0, 1], [1, 1], [1, 0]]
+
+
+@pytest.mark.parametrize("dims,bits", [(2, 3), (3, 2), (3, 4), (3, 7)])
+def test_hilbert_decode_inverts_encode(dims, bits):
+    # Two separate restatements of the package's published steps must invert
+    # each other: the encoder's loop orders, axis order and exchange step are
+    # what the decoder undoes (3 x 7 bits: the cfg1/cfg2 grids' bit count).
+    side = 1 << bits
+    if side ** dims <= 1 << 16:
+        grids = np.meshgrid(*[np.arange(side)] * dims, indexing="ij")
+        pts = np.stack([g.reshape(-1) for g in grids], axis=1)
+    else:
+        pts = np.random.default_rng(3).integers(0, side, size=(50000, dims))
+    codes = orc.hilbert_encode(pts, dims, bits)
+    assert np.array_equal(orc.hilbert_decode(codes, dims, bits), pts)
+    assert np.array_equal(orc.hilbert_encode(orc.hilbert_decode(codes, dims, bits), dims, bits), codes)
+
+
 @pytest.mark.parametrize("dims,bits", [(2, 3), (3, 2), (3, 3)])
 def test_hilbert_curve_invariants_on_full_cubes(dims, bits):
     side = 1 << bits
