@@ -361,6 +361,25 @@ __global__ void __launch_bounds__(256) score_topk_kernel(ScoreParams p) {
   }
 }
 
+// (head, workgroup within the head) of this workgroup in a grid of
+// (workgroups per head) x (heads). Workgroups are dispatched round-robin over
+// the 8 XCDs in linear order; when the heads divide evenly, XCD x takes heads
+// x, x + 8, ... whole, so the workgroups that stream one head's pooled keys
+// share one L2 instead of fetching the same chunks into eight (cfg1: 1/8 of
+// them on each XCD, 2.08 GB leaving L2 per launch for 0.64 GB of inputs and
+// workspace).
+__device__ __forceinline__ void head_major_xcd(int& h, int& wgx) {
+  const int nx = gridDim.x, heads = gridDim.y;
+  if ((heads & 7) != 0) {
+    h = blockIdx.y;
+    wgx = blockIdx.x;
+    return;
+  }
+  const int lin = blockIdx.y * nx + blockIdx.x, i = lin >> 3;
+  h = (lin & 7) + 8 * (i / nx);
+  wgx = i - (i / nx) * nx;
+}
+
 // Wide variant: each of the four waves owns its own 32 query tiles (G = 4 *
 // 32 / TPB query blocks per workgroup) and every 32-tile chunk of pooled keys
 // (hi and lo) is copied once into LDS, double-buffered, for all four waves:
@@ -386,8 +405,9 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
   __shared__ float inv_z[ONE_PASS ? 128 : 1];  // one pass: 1/Z of the workgroup's query tiles
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const Policy& pol = p.pol;
-  const int h = blockIdx.y;
-  const int qb0 = blockIdx.x * G;
+  int h, wgx;
+  head_major_xcd(h, wgx);
+  const int qb0 = wgx * G;
   // [G][Kb] block sums of this workgroup's query blocks
   float* bsum = GB ? (p.scores_out ? p.scores_out + (static_cast<int64_t>(h) * pol.scored_rows + qb0) * pol.Kb
                                    : nullptr)
@@ -487,7 +507,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
       // contiguous 128-byte line. U(kb) is this lane's tile's sum for key block kb.
       constexpr int WG_TILES = G * TPB;
       float* const ubase = p.tile_sums +
-                           (static_cast<int64_t>(h) * gridDim.x + blockIdx.x) * p.tile_cols * WG_TILES + w * 32 + l32;
+                           (static_cast<int64_t>(h) * gridDim.x + wgx) * p.tile_cols * WG_TILES + w * 32 + l32;
       auto U = [&](int kb) -> float& { return ubase[static_cast<int64_t>(kb) * WG_TILES]; };
       constexpr int BPC = ROWS / TPB;  // key blocks per chunk
       constexpr int NST = BPC / 2;     // key-block sums one lane stores per chunk
@@ -702,7 +722,7 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
     float iz[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) iz[i] = inv_z[w * 32 + 4 * sub + i];
-    const float* src = p.tile_sums + (static_cast<int64_t>(h) * gridDim.x + blockIdx.x) * p.tile_cols * WG_TILES +
+    const float* src = p.tile_sums + (static_cast<int64_t>(h) * gridDim.x + wgx) * p.tile_cols * WG_TILES +
                        w * 32 + 4 * sub;
     const int rs = max(1, min(QBW, ROW_CAP / pol.Kb));  // rows per group
     int row_beg[QBW];  // CSR starts of the wave's rows, loaded ahead of the sweep
