@@ -203,13 +203,13 @@ def test_topk_from_scores_hunyuan_policy(dev, video, text, ratio):
     assert torch.equal(ops.csr_to_mask(row_ptr, col_idx, heads, pol.q_blocks, pol.k_blocks).cpu(), want)
 
 
-@pytest.mark.parametrize("d,tile,video,text", [(128, 16, 4 * 16 * 16, 0), (128, 16, 3 * 20 * 21, 0),
-                                               (64, 16, 4 * 16 * 16, 0), (128, 32, 2000, 0),
-                                               (128, 16, 2000, 100), (64, 32, 1500, 100),
-                                               (128, 16, 20 * 128 + 16, 120)])  # last scored row dense, alone in its group
-def test_block_score_topk_matches_oracle(dev, d, tile, video, text):
+@pytest.mark.parametrize("d,tile,video,text,heads", [
+    (128, 16, 4 * 16 * 16, 0, 2), (128, 16, 3 * 20 * 21, 0, 2), (64, 16, 4 * 16 * 16, 0, 2), (128, 32, 2000, 0, 2),
+    (128, 16, 2000, 100, 2), (64, 32, 1500, 100, 2),
+    (128, 16, 20 * 128 + 16, 120, 2),  # last scored row dense, alone in its group
+    (128, 16, 3000, 0, 8), (128, 16, 2000, 100, 16)])  # heads divisible by 8: whole heads per XCD
+def test_block_score_topk_matches_oracle(dev, d, tile, video, text, heads):
     from dfsattn_amd.workloads import DfsConfig, synth_qkv
-    heads = 2
     cfg = DfsConfig("t", (1, 1, video), heads, d, torch.bfloat16, text_len=text, tile=tile, seed=3)
     q, k, v = synth_qkv(cfg)
     length = video + text
@@ -231,11 +231,17 @@ def test_block_score_topk_matches_oracle(dev, d, tile, video, text):
         orc.mask_from_scores_hunyuan(got, 0.3, length, video)
     assert torch.equal(mask.cpu().bool(), sel)
     assert torch.equal(ops.csr_to_mask(row_ptr, col_idx, heads, pol.q_blocks, pol.k_blocks).cpu(), sel)
-    # and agrees with the oracle's own fp32 mask up to near-ties
+    # and agrees with the oracle's own fp32 mask wherever the k-th and
+    # (k+1)-th oracle scores of a row are further apart than twice the
+    # measured score error
     ref_sel = orc.mask_from_scores_wan(ref, 0.3) if text == 0 else \
         orc.mask_from_scores_hunyuan(ref, 0.3, length, video)
-    agree = (sel == ref_sel).float().mean().item()
-    assert agree > 0.995, agree
+    err = float((got - ref).abs().max())
+    for h in range(heads):
+        for r in range(ref.shape[1]):
+            if not torch.equal(sel[h, r], ref_sel[h, r]):
+                top = torch.sort(ref[h, r, :pol.n_cand], descending=True).values
+                assert float(top[pol.k_pick - 1] - top[pol.k_pick]) <= 2 * err, (h, r, err)
 
 
 @pytest.mark.parametrize("video,text", [(4 * 16 * 16 * 4, 0), (2000, 100)])
