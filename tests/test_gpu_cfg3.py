@@ -4,8 +4,9 @@ the first 12 real steps dense, then dfs_attention with skip 12, interval 12
 and the step counter counting CFG passes (attention_wan.py:41-66, 432-470,
 792-800). Checks the refresh steps and their top-k sizes for sparsity 0.3
 with the reference's default decay 0.1 and without decay, that cached calls
-reuse the refreshed columns bit for bit, the fresh selection against the
-oracle's fp32 scores, and sampled query blocks of one refresh call and one
+reuse the refreshed columns bit for bit, the fresh selection (bit-exact
+from the GPU's own fp32 scores, and against the oracle's fp32 scores up to
+near-ties), and sampled query blocks of one refresh call and one
 cached call against fp32 masked attention (fp32 output, 1e-3 mean-rel)."""
 import pytest
 import torch
@@ -39,6 +40,36 @@ def _check_output(dev, entry, q, k, v, full, perm_d, lay, out_bf16, label):
     # the call's own (bf16) output is the same computation, rounded
     got = out_bf16[:, heads].cpu()[:, :, full][:, :, rows].float()
     assert _rel(got, g32) < 4e-3
+
+
+def _check_selection(dev, entry, q, k, v, full, perm_d, lay, kpick, label):
+    """Head 0 of a refresh: the cached mask is the top-k of the GPU's own fp32
+    block scores (bit-exact), and every row that selects differently from the
+    oracle's fp32 scores has its k-th and (k+1)-th oracle scores closer than
+    twice the measured score error."""
+    from dfsattn_amd import ops
+    from dfsattn_amd.layout import TopkPolicy
+    Kb = lay.k_blocks
+    pol = TopkPolicy(lay.q_blocks, Kb, lay.q_blocks, Kb, kpick, Kb, lay.q_blocks)
+    prep = ops.prepare_qkv(q[:, :1], k[:, :1], v[:, :1], perm_d, lay)
+    row_ptr = torch.from_numpy(pol.row_ptr(1)).to(dev)
+    _, scores, _ = ops.block_score_topk(prep, pol, row_ptr, want_scores=True)
+    got = scores.cpu()
+    mask = entry["block_mask"][:1].cpu()
+    assert torch.equal(mask, orc.select_topk(got, kpick))
+    qp = orc.apply_permutation(q[:, :1].float().cpu(), full)
+    kp = orc.apply_permutation(k[:, :1].float().cpu(), full)
+    ref_scores = orc.block_scores(qp, kp, lay.tile, 128, None, head_chunk=1)
+    ref_sel = orc.select_topk(ref_scores, kpick)
+    err = float((got - ref_scores).abs().max())
+    gaps = []
+    for r in range(ref_scores.shape[1]):
+        if not torch.equal(mask[0, r], ref_sel[0, r]):
+            top = torch.sort(ref_scores[0, r], descending=True).values
+            gaps.append(float(top[kpick - 1] - top[kpick]))
+    print(f"{label}: {len(gaps)} of {ref_scores.shape[1]} rows select differently from the oracle's fp32 scores; "
+          f"max score error {err:.2e}, largest gap among them {max(gaps, default=0.0):.2e}", flush=True)
+    assert all(g <= 2 * err for g in gaps), (gaps, err)
 
 
 @pytest.mark.parametrize("dcrt,expect", [(0.1, {12: 177, 24: 118, 36: 59}),
@@ -80,13 +111,7 @@ def test_mask_cache_regime_at_cfg1_shape(dev, dcrt, expect):
             refreshes[t] = kpick
             kept_cols = entry["col_idx"].clone()
             if t == 24:  # the fresh selection of head 0 against the oracle's fp32 scores
-                qp = orc.apply_permutation(q[:, :1].float().cpu(), full)
-                kp = orc.apply_permutation(k[:, :1].float().cpu(), full)
-                ref_scores = orc.block_scores(qp, kp, cfg.tile, 128, None, head_chunk=1)
-                ref_mask = orc.mask_from_scores_torch(ref_scores, kpick)
-                agree = float((entry["block_mask"][:1].cpu() == ref_mask).all(-1).float().mean())
-                print(f"dcrt {dcrt} step {t}: rows selected as from the oracle's scores: {agree:.4f}", flush=True)
-                assert agree >= 0.98
+                _check_selection(dev, entry, q, k, v, full, perm_d, lay, kpick, f"dcrt {dcrt} step {t}")
             if t == 12:
                 _check_output(dev, entry, q, k, v, full, perm_d, lay, out, f"dcrt {dcrt} refresh step {t}")
         else:
