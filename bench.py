@@ -9,9 +9,13 @@ the fused inverse permutation.
 
 Prints one JSON line (metric = ms per call, lower is better) with the
 roofline of the attention kernel, per-phase kernel times and a CPU baseline
-(the fp32 oracle on a bounded sample of the same inputs, scaled up). Two
-side measurements ride on the same line: the attention kernel on bf16
-operands (the reference kernel's operand precision) over the same mask, and
+(the fp32 oracle on a bounded sample of the same inputs, scaled up). The
+phase times (and so the roofline's achieved rate) come from HIP event pairs
+that the call's own phase recorder places around prepare, score + top-k and
+attention in every timed step. Two side measurements ride on the same line:
+the attention kernel on bf16 operands (the reference kernel's operand
+precision) over the same mask, beside the default f16 operands timed in the
+same stretch, and
 a less local mask at the same density (K drawn from a field of its own, so a
 row's kept blocks spread over the whole row): its whole-call median and its
 attention kernel time.
@@ -98,6 +102,12 @@ def run_gpu(args):
         step()
         torch.cuda.synchronize()
         log(f"warmup step {i + 1}/{args.warmup} done")
+    # The timed steps run with the call's own phase recorder on: it records a
+    # HIP event pair on the current stream (the stream the kernels run on)
+    # around the prepare, score + top-k and attention phases of every call,
+    # and never waits for the device, so the phase times come from the timed
+    # region itself.
+    DFS_Attention.set_record_timing(True)
     t0 = time.perf_counter()
     e0, e1 = _events()
     e0.record()
@@ -107,7 +117,19 @@ def run_gpu(args):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ms_per_step = e0.elapsed_time(e1) / args.steps
+    spans = DFS_Attention.timing_recorder.rows()
+    DFS_Attention.set_record_timing(False)
     log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/call")
+    phase_of = {"qkv_permute": "prepare", "topk_mask": "score_topk", "attention_execution": "attention"}
+    ev = {name: [] for name in phase_of.values()}
+    for span in spans:
+        if span["phase"] in phase_of:
+            ev[phase_of[span["phase"]]].append(span["elapsed_ms"])
+    assert all(len(v_) == args.steps for v_ in ev.values()), {k_: len(v_) for k_, v_ in ev.items()}
+    phase_ms = {k_: float(np.mean(v_)) for k_, v_ in ev.items()}
+    log(f"phase times over the timed steps (ms): {phase_ms}")
+    entry = next(iter(DFS_Attention._cached_metadata.values()))
+    row_ptr, col_idx = entry["row_ptr"], entry["col_idx"]  # the last timed call's mask
     # Median of per-call event pairs over at least 50 further calls.
     per_call = []
     for _ in range(max(50, args.steps)):
@@ -121,33 +143,10 @@ def run_gpu(args):
     median_ms = per_call[len(per_call) // 2]
     log(f"median of {len(per_call)} calls: {median_ms:.3f} ms")
 
-    # Per-kernel times of the same call, each bracketed by events on the
-    # stream the kernels run on (the current stream), averaged over steps.
     layout = ScoringLayout(L, L, cfg.tile)
     pol = wan_policy(layout, cfg.sparsity)
     perm_d = ops.device_perm(video_perm, dev)
-    row_ptr = torch.from_numpy(pol.row_ptr(cfg.heads)).to(dev)
     reps = max(3, args.steps)
-    ev = {name: [] for name in ("prepare", "score_topk", "attention")}
-    for _ in range(reps):
-        a0, a1 = _events(); b1, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        # Keep the GPU busy (about 1 ms) while the host enqueues the three
-        # phases, so each event pair brackets GPU work only, not the host's
-        # launch latency after the synchronisation.
-        torch.cuda._sleep(2_000_000)
-        a0.record()
-        prep = ops.prepare_qkv(q, k, v, perm_d, layout)
-        a1.record()
-        col_idx, _, _ = ops.block_score_topk(prep, pol, row_ptr)
-        b1.record()
-        ops.bsa_fwd(prep, row_ptr, col_idx, out_perm=perm_d)
-        c1.record()
-        torch.cuda.synchronize()
-        ev["prepare"].append(a0.elapsed_time(a1))
-        ev["score_topk"].append(a1.elapsed_time(b1))
-        ev["attention"].append(b1.elapsed_time(c1))
-    phase_ms = {k_: float(np.mean(v_)) for k_, v_ in ev.items()}
-    log(f"phase times (ms): {phase_ms}")
     flops = csr_flops(row_ptr.cpu().numpy(), col_idx.cpu().numpy(), cfg.heads, L, cfg.head_dim)
     att_tflops = flops / (phase_ms["attention"] * 1e-3) / 1e12
     D = cfg.head_dim
@@ -155,7 +154,6 @@ def run_gpu(args):
     prep_bytes = 3 * 2 * tensor_bytes  # read + write of Q, K, V (pooled outputs are ~1/16 extra)
     score_flop = 2 * layout.q_tiles * layout.k_tiles * D * cfg.heads
 
-    del prep
     side = {}
     if not args.headline_only:
         side = _side_measurements(args, cfg, dev, q, k, v, video_perm, layout, pol, perm_d, row_ptr, col_idx, flops,
@@ -202,11 +200,14 @@ def _side_measurements(args, cfg, dev, q, k, v, video_perm, layout, pol, perm_d,
         return float(np.mean(times))
 
     # The same mask on bf16 operands (Q, K, V and P in bf16, the reference
-    # kernel's operand precision) beside the default f16 operands.
+    # kernel's operand precision) beside the default f16 operands, timed in
+    # the same stretch so that both see the same clock.
+    prep_f16 = ops.prepare_qkv(q, k, v, perm_d, layout, pool=False)
     prep16 = ops.prepare_qkv(q, k, v, perm_d, layout, operand_dtype=torch.bfloat16, pool=False)
+    f16_ms = attention_ms(prep_f16, col_idx)
     bf16_ms = attention_ms(prep16, col_idx)
-    del prep16
-    log(f"attention on bf16 operands: {bf16_ms:.3f} ms")
+    del prep16, prep_f16
+    log(f"attention on bf16 operands: {bf16_ms:.3f} ms (f16 operands in the same stretch: {f16_ms:.3f} ms)")
 
     # A less local mask at the same density: K from a field of its own, so
     # the kept blocks of a row spread over the whole row instead of clustering
@@ -247,7 +248,8 @@ def _side_measurements(args, cfg, dev, q, k, v, video_perm, layout, pol, perm_d,
     del prep_n, qn, kn, vn
     return {
         "attention_bf16_operands": {"ms": round(bf16_ms, 3), "tflops": round(flops / (bf16_ms * 1e-3) / 1e12, 1),
-                                    "frac": round(flops / (bf16_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
+                                    "frac": round(flops / (bf16_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                    "f16_operands_ms_same_stretch": round(f16_ms, 3)},
         "less_local_mask": less_local,
     }
 
