@@ -384,3 +384,38 @@ def test_wan_edge_shapes_match_oracle(dev, grid, heads, d, dtype, sparsity):
     ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
     assert _rel(out.cpu(), ref) < 4e-3
     assert float((out.cpu().float() - ref).abs().max()) < 2e-2
+
+
+def test_bf16_operand_setting_through_the_call(dev):
+    """DFS_Attention.operand_dtype = bf16 (the reference kernel's operand
+    precision): the whole call and the dense path keep Q, K, V and P in
+    bf16, select the same mask as the default call, and match fp32 attention
+    on that mask within the bf16 operand class (P rounded to bf16: about
+    1.5e-3 mean-rel, plus the bf16 output rounding)."""
+    from dfsattn_amd.attention_wan import DFS_Attention, dfs_attention
+    from dfsattn_amd.fullattention import full_attention
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+
+    cfg = DfsConfig("bf16ops", (3, 16, 20), 2, 128, torch.bfloat16, seed=17)
+    q, k, v = synth_qkv(cfg)
+    perm = hilbert3d_perm(*cfg.grid)
+    kw = dict(step_idx=24, skip_steps=12, cache_interval=12, sparsity=0.3, sparsity_dcrt=0.0, tile_size=16,
+              video_perm=perm)
+    default = dfs_attention(q.to(dev), k.to(dev), v.to(dev), layer_idx=0, **kw)
+    mask_default = DFS_Attention._cached_metadata[(0, "native", 128, 16, 16)]["block_mask"].cpu()
+    DFS_Attention.operand_dtype = torch.bfloat16
+    try:
+        out = dfs_attention(q.to(dev), k.to(dev), v.to(dev), layer_idx=1, **kw)
+        dense = full_attention(q.to(dev), k.to(dev), v.to(dev), mode="flash",
+                               operand_dtype=DFS_Attention.operand_dtype)
+    finally:
+        DFS_Attention.operand_dtype = None
+    mask = DFS_Attention._cached_metadata[(1, "native", 128, 16, 16)]["block_mask"].cpu()
+    assert torch.equal(mask, mask_default)  # scoring does not depend on the attention operands
+    p, inv = orc.full_permutation(perm, q.shape[2])
+    ref = orc.masked_attention(*(orc.apply_permutation(x.float(), p) for x in (q, k, v)), mask)[:, :, inv]
+    assert out.dtype == torch.bfloat16 and not torch.equal(out, default)
+    assert _rel(out.cpu(), ref) < 5e-3 and float((out.cpu().float() - ref).abs().max()) < 2e-2
+    ref_dense = orc.dense_attention(q.float(), k.float(), v.float())
+    assert _rel(dense.cpu(), ref_dense) < 5e-3
