@@ -378,6 +378,24 @@ def test_bsa_fwd_matches_masked_dense(dev, scale, d, length, density, pv):
         assert mean_rel(out, dense) <= tol
 
 
+@pytest.mark.parametrize("length", [127, 129, 255, 257, 383, 641])
+@pytest.mark.parametrize("heads,d", [(1, 128), (3, 64), (5, 128)])
+def test_bsa_fwd_ragged_lengths(dev, length, heads, d):
+    """Lengths just under and over multiples of the 128-token block (the
+    last block's keys masked, its rows dropped) with odd head counts, at the
+    output contract on fp32 output."""
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+    cfg = DfsConfig("t", (1, 1, length), heads, d, torch.bfloat16, seed=length + heads)
+    q, k, v = synth_qkv(cfg)
+    nb = math.ceil(length / 128)
+    mask = torch.rand((heads, nb, nb), generator=torch.Generator().manual_seed(length)) < 0.5
+    mask[:, :, nb - 1] = True  # every row sees the partial block
+    out = _run_bsa(dev, q, k, v, mask, torch.float16, torch.float32)
+    ref = orc.masked_attention(q, k, v, mask)
+    assert out.shape == ref.shape
+    assert float((out - ref).abs().max()) <= 2e-2 and mean_rel(out, ref) <= 1e-3
+
+
 def test_bsa_fwd_bf16_out_and_fused_unpermute(dev):
     from dfsattn_amd.workloads import DfsConfig, synth_qkv
     heads, d, length = 2, 128, 1000
