@@ -285,6 +285,7 @@ def run_cfg2(args):
         step()
         torch.cuda.synchronize()
         log(f"warmup step {i + 1}/{args.warmup} done")
+    DFS_Attention.set_record_timing(True)  # phase event pairs inside the timed calls
     e0, e1 = _events()
     e0.record()
     for _ in range(args.steps):
@@ -292,12 +293,17 @@ def run_cfg2(args):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
+    spans = DFS_Attention.timing_recorder.rows()
+    DFS_Attention.set_record_timing(False)
+    phase_of = {"qkv_permute": "prepare", "topk_mask": "score_topk", "attention_execution": "attention"}
+    phase_ms = {name: float(np.mean([r["elapsed_ms"] for r in spans if r["phase"] == ph]))
+                for ph, name in phase_of.items()}
     entry = next(iter(DFS_Attention._cached_metadata.values()))
     flops = csr_flops(entry["row_ptr"].cpu().numpy(), entry["col_idx"].cpu().numpy(), cfg.heads, cfg.seq_len,
                       cfg.head_dim)
     DFS_Attention.clear_cache()
     _dfs_attention_instances.clear()
-    log(f"cfg2: {ms:.3f} ms/call, {flops / ms / 1e9:.1f} effective TFLOP/s")
+    log(f"cfg2: {ms:.3f} ms/call, {flops / ms / 1e9:.1f} effective TFLOP/s; phases (ms) {phase_ms}")
     pad = ("" if args.text_valid is None else
            f", text padding: {args.text_valid} valid text tokens, cu_seqlens [0, valid, L] (FLOP counted on the "
            "whole-sequence mask)")
@@ -309,7 +315,10 @@ def run_cfg2(args):
                                    "d128, tile 16, block 128, hilbert3d, sparsity 0.3, fresh mask per call" + pad,
                        "global_batch": 1, "seq_len": cfg.seq_len, "parallelism": "none (1 GPU)"},
             "effective_tflops": round(flops / ms / 1e9, 1), "kept_flop": flops,
-            "frac_of_bf16_peak": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4)}
+            "frac_of_bf16_peak": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+            "phases_ms": {k_: round(v_, 3) for k_, v_ in phase_ms.items()},
+            "attention_kernel": {"tflops": round(flops / phase_ms["attention"] / 1e9, 1),
+                                 "frac": round(flops / phase_ms["attention"] / 1e9 / PEAK_BF16_TFLOPS, 4)}}
 
 
 def run_cfg3(args):
