@@ -1,8 +1,8 @@
-"""The reference-side bindings printed in INTEGRATION.md, run exactly as
-printed (the Python blocks are read from the file; only the library path
-placeholder is pointed at this build): the ctypes replacement of
-block_sparse_attn_func (attention_wan.py:335-391) and the RoPE / RMSNorm
-shims of replace_wan.py:24-66, against the oracle."""
+"""The reference-side bindings that the repository's integration guide
+prints, run exactly as printed (the Python blocks are read from the guide
+at DOC; only the library path placeholder is pointed at this build): the
+ctypes replacement of block_sparse_attn_func (attention_wan.py:335-391) and
+the RoPE / RMSNorm shims of replace_wan.py:24-66, against the oracle."""
 import math
 import os
 import re
