@@ -309,6 +309,31 @@ def test_block_score_topk_workspace_checks(dev):
     assert torch.equal(col, with_scores)
 
 
+@pytest.mark.parametrize("heads,length,text", [(2, 3000, 0), (8, 2000, 0), (2, 2000, 100)])
+def test_block_score_topk_all_tied_keeps_lowest_columns(dev, heads, length, text):
+    """Q = 0 makes every logit 0, so every scored block sums exactly the same
+    (its 64 tile pairs of 1/Z each): the top-k is one big tie, and the fused
+    selection (one-pass and two-pass forms, whole heads per XCD at 8 heads)
+    keeps the lowest candidate columns, as a stable descending sort does."""
+    video = length - text
+    q = torch.zeros(1, heads, length, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.randn(1, heads, length, 128, generator=torch.Generator().manual_seed(4)).bfloat16().to(dev)
+    layout = ScoringLayout(length, video, 16)
+    pol = wan_policy(layout, 0.3) if text == 0 else hunyuan_policy(layout, 0.3)
+    row_ptr = torch.from_numpy(pol.row_ptr(heads)).to(dev)
+    prep = ops.prepare_qkv(q, k, k, torch.arange(length, dtype=torch.int32, device=dev), layout)
+    want = torch.zeros((heads, pol.q_blocks, pol.k_blocks), dtype=torch.bool)
+    want[:, :pol.dense_row, :pol.k_pick] = True
+    want[:, :pol.dense_row, pol.dense_col:] = True
+    want[:, pol.dense_row:] = True
+    for one_pass in (True, False):
+        _, scores, mask = ops.block_score_topk(prep, pol, row_ptr, want_scores=True, want_mask=True,
+                                               one_pass=one_pass)
+        got = scores.cpu()[:, :min(pol.scored_rows, pol.dense_row), :pol.n_cand]
+        assert bool((got == got[0, 0, 0]).all())  # one tie over every candidate
+        assert torch.equal(mask.cpu().bool(), want), one_pass
+
+
 @pytest.mark.parametrize("direction", ["rising", "falling"])
 @pytest.mark.parametrize("tile,one_pass", [(16, True), (32, True), (16, False), (32, False)])
 def test_block_scores_with_far_apart_logits(dev, direction, tile, one_pass):
