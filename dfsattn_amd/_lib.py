@@ -23,12 +23,12 @@ SIGNATURES = {
     "dfs_hilbert3d_perm": [_i64, _i64, _i64, _p],
     "dfs_permute_gather": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
     "dfs_permute_scatter": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
-    "dfs_prepare_qkv": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _i64, _i32,
+    "dfs_prepare_qkv": [_p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _i32,
                         _p, _p, _p, _p, _p, _p, _p, _p, _p],
-    "dfs_block_score_topk_workspace_size": [_i64, _i64, _i64, _i64],
-    "dfs_block_score_topk": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+    "dfs_block_score_topk_workspace_size": [_i64, _i64, _i64, _i64, _i64],
+    "dfs_block_score_topk": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _p],
-    "dfs_block_score_topk_noalloc": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+    "dfs_block_score_topk_noalloc": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _i64, _i64, _i64, _p, _p, _p, _p],
     "dfs_topk_from_scores": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p],
     "dfs_prepare_fixup": [_p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p],
@@ -44,7 +44,7 @@ SIGNATURES = {
     "dfs_gated_residual": [_p, _p, _p, _i64, _i64, _i32, _p, _p],
 }
 _RESTYPES = {"dfs_last_error": ctypes.c_char_p, "dfs_block_score_topk_workspace_size": ctypes.c_int64}
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib = None

@@ -102,9 +102,10 @@ class DfsCore:
         return perm
 
     def _layout(self, seq_len: int) -> ScoringLayout:
-        if self.q_tile_size != self.k_tile_size:
-            raise NotImplementedError("the fused scorer uses one tile size for queries and keys")
-        return ScoringLayout(seq_len, self._video_len(seq_len), self.q_tile_size, self.block_size)
+        """Scoring layout with the instance's query and key tile sizes (each
+        must divide the block, attention_wan.py:227-228)."""
+        return ScoringLayout(seq_len, self._video_len(seq_len), self.q_tile_size, self.block_size,
+                             k_tile=self.k_tile_size)
 
     # --- checks ---------------------------------------------------------------
     def _check_call(self, q, k, v, attn_mask, causal, drop_rate, batch_size):

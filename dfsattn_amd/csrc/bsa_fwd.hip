@@ -554,9 +554,14 @@ __device__ __forceinline__ void bsa_split_block(const uint16_t* __restrict__ q, 
     for (int s = 0; s < D / 16; ++s) asm volatile("" ::"v"(qf[s]));
     block_barrier();
     auto col_at = [&](int t) -> int { return __builtin_amdgcn_readfirstlane(cols[t]); };
-    int kb = col_at(0);
-    kcopy.template issue<K_LOADS>(krs, kb * TILE_BYTES, k_base, ws);
-    vcopy.template issue<V_LOADS>(vrs, kb * TILE_BYTES, v_base, ws);
+    // n == 0: every kept column lies past this sequence's keys (a shorter
+    // key segment), so cols holds nothing to copy; the row stays empty.
+    // n is the same for every wave (read from LDS after a barrier).
+    int kb = n > 0 ? col_at(0) : 0;
+    if (n > 0) {
+      kcopy.template issue<K_LOADS>(krs, kb * TILE_BYTES, k_base, ws);
+      vcopy.template issue<V_LOADS>(vrs, kb * TILE_BYTES, v_base, ws);
+    }
 
     for (int t = 0; t < n; ++t) {
       // After the last block the copies reload the current block into the
@@ -823,6 +828,9 @@ __global__ void __launch_bounds__(256) bsa_segment_kernel(const uint16_t* __rest
     for (int i = 0; i < RG; ++i) {
       const int r = r0 + i;
       if (r >= p.L) break;
+      // A group may straddle the second sequence's end: its rows past cq2
+      // were scored with q = 0 and belong to no sequence (zero, lse -inf).
+      if (r >= cq2) l[i] = 0.f;
       const float inv = l[i] > 0.f ? sv / l[i] : 0.f;
       const int orow = out_perm ? out_perm[r] : r;
       const int64_t ob = (static_cast<int64_t>(h) * p.Lo + orow) * D + lane * DPL;

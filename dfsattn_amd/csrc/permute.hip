@@ -110,7 +110,8 @@ struct PrepParams {
   int vpad;      // zero rows inserted after the video in the scoring layout
   int q_tiles;   // pooled query tiles (video part of the scoring layout)
   int k_tiles;   // pooled key tiles (whole scoring layout)
-  int tile;      // tokens per tile
+  int tile_q;    // tokens per query tile
+  int tile_k;    // tokens per key tile
   int in_f16;    // q/k/v are f16 (else bf16)
   int convert;   // bf16 inputs, f16 operands: q_perm, k_perm and v_t get converted values
   int pool;      // write pooled tiles
@@ -147,7 +148,9 @@ __device__ __forceinline__ void add_chunk(float acc[8], const uint4& v, bool f16
 // execution layout and writes the tile mean as a bf16 hi/lo pair. Zero rows of
 // the scoring layout count toward the mean, as in the reference's zero-padded
 // .view(...).mean(3). Tiles past the query tiles still gather text rows of Q.
-// Block bx of nbx for (head h of H, tensor Q or K).
+// Q and K have their own tile sizes (q_tile_size, k_tile_size); either way
+// the tiles of a tensor cover the whole scoring layout, every row gathered
+// once. Block bx of nbx for (head h of H, tensor Q or K).
 template <int D>
 __device__ __forceinline__ void prep_qk_tiles(const PrepParams& p, int bx, int nbx, int h, int H, bool is_k) {
   constexpr int CPR = D / 8;        // 16-byte chunks per row
@@ -164,8 +167,9 @@ __device__ __forceinline__ void prep_qk_tiles(const PrepParams& p, int bx, int n
       store_stream(dst + static_cast<int64_t>(p.L) * CPR + i, make_uint4(0, 0, 0, 0));
   }
 
+  const int tile = is_k ? p.tile_k : p.tile_q;
   const int t = bx * 4 + wave;
-  if (t >= p.k_tiles) return;
+  if (t * tile >= p.R) return;  // past the scoring layout (R tokens) of this tensor
   const int c = lane % CPR;
   const int g = lane / CPR;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -173,13 +177,13 @@ __device__ __forceinline__ void prep_qk_tiles(const PrepParams& p, int bx, int n
   // Rows in batches of four passes: the permutation reads of a batch, then
   // its row reads, are all in flight before the first store.
   constexpr int BATCH = 4;
-  for (int r0 = g; r0 < p.tile; r0 += BATCH * RPP) {
+  for (int r0 = g; r0 < tile; r0 += BATCH * RPP) {
     int xs[BATCH], ss[BATCH];
     uint4 val[BATCH];
 #pragma unroll
     for (int b = 0; b < BATCH; ++b) {
       const int r = r0 + b * RPP;
-      xs[b] = r < p.tile ? scoring_to_exec(t * p.tile + r, p) : -1;
+      xs[b] = r < tile ? scoring_to_exec(t * tile + r, p) : -1;
       ss[b] = xs[b] >= 0 ? p.perm[xs[b]] : -1;
     }
 #pragma unroll
@@ -202,7 +206,7 @@ __device__ __forceinline__ void prep_qk_tiles(const PrepParams& p, int bx, int n
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] += __shfl_xor(acc[i], off);
   if (g != 0) return;
-  const float inv = 1.0f / static_cast<float>(p.tile);
+  const float inv = 1.0f / static_cast<float>(tile);
   uint32_t hi[8], lo[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -409,7 +413,7 @@ int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst, int64_t
 
 int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* perm,
                     int64_t heads, int64_t seq_len, int64_t head_dim, int dtype,
-                    int64_t video_len, int64_t tile_size, int operand_dtype, void* q_perm,
+                    int64_t video_len, int64_t q_tile_size, int64_t k_tile_size, int operand_dtype, void* q_perm,
                     void* k_perm, void* v_t, uint16_t* q_pool_hi, uint16_t* q_pool_lo,
                     uint16_t* k_pool_hi, uint16_t* k_pool_lo, int32_t* overflow,
                     dfs_stream_t stream) {
@@ -427,8 +431,10 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* 
   DFS_REQUIRE(seq_len > 0 && video_len > 0 && video_len <= seq_len,
               "dfs_prepare_qkv: need 0 < video_len=%lld <= seq_len=%lld", (long long)video_len,
               (long long)seq_len);
-  DFS_REQUIRE(tile_size > 0 && kBlock % tile_size == 0,
-              "dfs_prepare_qkv: tile_size=%lld must divide 128", (long long)tile_size);
+  DFS_REQUIRE(q_tile_size > 0 && kBlock % q_tile_size == 0,
+              "dfs_prepare_qkv: q_tile_size=%lld must divide 128", (long long)q_tile_size);
+  DFS_REQUIRE(k_tile_size > 0 && kBlock % k_tile_size == 0,
+              "dfs_prepare_qkv: k_tile_size=%lld must divide 128", (long long)k_tile_size);
   const int64_t kb = (seq_len + kBlock - 1) / kBlock;
   const int64_t vb = (video_len + kBlock - 1) / kBlock;
   const int64_t vpad = vb * kBlock - video_len;
@@ -459,15 +465,18 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* 
   p.Lv = static_cast<int>(video_len);
   p.R = static_cast<int>(kb * kBlock);
   p.vpad = static_cast<int>(vpad);
-  p.tile = static_cast<int>(tile_size);
-  p.q_tiles = static_cast<int>(vb * kBlock / tile_size);
-  p.k_tiles = static_cast<int>(kb * kBlock / tile_size);
+  p.tile_q = static_cast<int>(q_tile_size);
+  p.tile_k = static_cast<int>(k_tile_size);
+  p.q_tiles = static_cast<int>(vb * kBlock / q_tile_size);
+  p.k_tiles = static_cast<int>(kb * kBlock / k_tile_size);
   p.in_f16 = dtype == DFS_DTYPE_F16;
   p.convert = (dtype == DFS_DTYPE_BF16 && operand_dtype == DFS_DTYPE_F16);
   p.pool = pool ? 1 : 0;
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  dim3 gqk(static_cast<unsigned>((p.k_tiles + 3) / 4), static_cast<unsigned>(heads), 2);
+  // Enough four-wave blocks for the smaller of the two tiles (more tiles).
+  const int64_t max_tiles = kb * kBlock / (q_tile_size < k_tile_size ? q_tile_size : k_tile_size);
+  dim3 gqk(static_cast<unsigned>((max_tiles + 3) / 4), static_cast<unsigned>(heads), 2);
   dim3 gv(static_cast<unsigned>(kb), static_cast<unsigned>(heads));
   if (head_dim == 128) {
     prep_qk_kernel<128><<<gqk, 256, 0, s>>>(p);

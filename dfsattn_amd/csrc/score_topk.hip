@@ -790,6 +790,135 @@ __global__ void __launch_bounds__(256, 2) score_topk_wide_kernel(ScoreParams p) 
   }
 }
 
+// Block sums of one 32 x 32 chunk of tile probabilities for TPBK key tiles
+// per block. pr[r] is this lane's exp2(s - M) for key tile acc_row(r, hl) of
+// the chunk and query tile l32, inv_z that query tile's 1/Z. The sum runs over
+// a block's key tiles inside the lane (across the lane halves too when a
+// block spans them), then 1/Z is applied, then the sum runs over the tpbq
+// lanes (query tiles) of a query block. store(qbl, kbl, v) is called by one
+// lane per (query block l32 / tpbq of the wave, key block kbl of the chunk).
+template <int TPBK, typename Store>
+__device__ __forceinline__ void chunk_block_sums(const float* pr, float inv_z, int tpbq, int l32, int hl,
+                                                 Store store) {
+  constexpr int NV = TPBK <= 4 ? 16 / TPBK : 32 / TPBK;  // key blocks this lane holds sums of
+  float v[NV];
+  if constexpr (TPBK <= 4) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const float* x = pr + i * TPBK;
+      if constexpr (TPBK == 1) v[i] = x[0];
+      else if constexpr (TPBK == 2) v[i] = x[0] + x[1];
+      else v[i] = (x[0] + x[1]) + (x[2] + x[3]);
+    }
+  } else {
+    constexpr int GPB = TPBK / 8;  // register groups of four per key block
+#pragma unroll
+    for (int b = 0; b < NV; ++b) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = b * GPB; g < (b + 1) * GPB; ++g) t += (pr[4 * g] + pr[4 * g + 1]) + (pr[4 * g + 2] + pr[4 * g + 3]);
+      v[b] = t + __shfl_xor(t, 32);  // the block's other half of key tiles
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] *= inv_z;
+  for (int off = 1; off < tpbq; off <<= 1)
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] += __shfl_xor(v[i], off);
+  if ((l32 & (tpbq - 1)) != 0 || (TPBK >= 8 && hl != 0)) return;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) store(l32 / tpbq, TPBK <= 4 ? acc_row(i * TPBK, hl) / TPBK : i, v[i]);
+}
+
+// Scoring and selection for any query and key tile sizes from 4 to 128
+// tokens (q_tile_size and k_tile_size independent, each dividing the block),
+// as the reference allows (attention_wan.py:227-246; attention_hyvideo.py:
+// 406-422). A plainer form of the wide kernel: each wave owns 32 query tiles
+// (32 / tpbq query blocks) and reads the pooled key chunks straight from
+// global memory; pass 1 builds each query tile's softmax normaliser, pass 2
+// recomputes the chunk scores into block sums in scores_out (which the caller
+// provides); then the workgroup's rows are selected. Same hi/lo-split
+// products as the tuned kernels, so the scores are as accurate.
+template <int D>
+__global__ void __launch_bounds__(256) score_topk_tiles_kernel(ScoreParams p, int tpbq, int tpbk) {
+  constexpr int CPR = D / 8;
+  __shared__ uint32_t hist[4][256];
+  const Policy& pol = p.pol;
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
+  const int qbw_n = 32 / tpbq;           // query blocks per wave
+  const int G = 4 * qbw_n;                // query blocks per workgroup
+  const int qb0 = blockIdx.x * G, qbw = qb0 + w * qbw_n;
+  const int rows_to_score = pol.scored_rows;  // scores_out holds every scored row
+  float* const bsum = p.scores_out + static_cast<int64_t>(h) * pol.scored_rows * pol.Kb;
+  if (qbw < rows_to_score) {
+    bf16x8 qh[D / 16], ql[D / 16];
+    const int qt = qbw * tpbq + l32;
+    const bool qv = qt < p.q_tiles;
+    load_q_prescaled<D>(p, qv, (static_cast<int64_t>(h) * p.q_tiles + (qv ? qt : 0)) * CPR + hl, qh, ql);
+    const int nchunks = (p.k_tiles + 31) / 32;
+    // Pass 1: normaliser of each query tile against a running maximum (log2 units).
+    float m = -INFINITY, z = 0.f;
+    for (int c = 0; c < nchunks; ++c) {
+      const f32x16 acc = score_chunk<D>(p, h, c, l32, hl, qh, ql);
+      float cm = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (c * 32 + acc_row(r, hl) < p.k_tiles) cm = fmaxf(cm, acc[r]);
+      const float mn = fmaxf(m, cm);
+      if (mn > -INFINITY) {
+        float sum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (c * 32 + acc_row(r, hl) < p.k_tiles) sum += exp2_fast(acc[r] - mn);
+        z = (m > -INFINITY ? z * exp2_fast(m - mn) : 0.f) + sum;
+        m = mn;
+      }
+    }
+    const float m_o = __shfl_xor(m, 32), z_o = __shfl_xor(z, 32);
+    const float M = fmaxf(m, m_o);
+    float Z = 0.f;
+    if (m > -INFINITY) Z += z * exp2_fast(m - M);
+    if (m_o > -INFINITY) Z += z_o * exp2_fast(m_o - M);
+    const float inv_z = Z > 0.f ? 1.0f / Z : 0.f;
+    // Pass 2: block sums of the tile probabilities.
+    const int bpc = 32 / tpbk;  // key blocks per chunk
+    for (int c = 0; c < nchunks; ++c) {
+      const f32x16 acc = score_chunk<D>(p, h, c, l32, hl, qh, ql);
+      float pr[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        pr[r] = c * 32 + acc_row(r, hl) < p.k_tiles ? exp2_fast(acc[r] - M) : 0.f;
+      auto store = [&](int qbl, int kbl, float val) {
+        const int qb = qbw + qbl, kb = c * bpc + kbl;
+        if (qb < rows_to_score && kb < pol.Kb) bsum[static_cast<int64_t>(qb) * pol.Kb + kb] = val;
+      };
+      switch (tpbk) {
+        case 1: chunk_block_sums<1>(pr, inv_z, tpbq, l32, hl, store); break;
+        case 2: chunk_block_sums<2>(pr, inv_z, tpbq, l32, hl, store); break;
+        case 4: chunk_block_sums<4>(pr, inv_z, tpbq, l32, hl, store); break;
+        case 8: chunk_block_sums<8>(pr, inv_z, tpbq, l32, hl, store); break;
+        case 16: chunk_block_sums<16>(pr, inv_z, tpbq, l32, hl, store); break;
+        default: chunk_block_sums<32>(pr, inv_z, tpbq, l32, hl, store); break;
+      }
+    }
+  }
+  __threadfence_block();  // the block sums in global memory are visible to the workgroup's loads
+  __syncthreads();
+  for (int g = w; g < G; g += 4) {
+    const int qb = qb0 + g;
+    if (qb >= pol.Qb) break;
+    const int64_t row = static_cast<int64_t>(h) * pol.Qb + qb;
+    int32_t* cols = p.col_idx + p.row_ptr[row];
+    uint8_t* mrow = p.mask_out ? p.mask_out + row * pol.Kb : nullptr;
+    if (qb >= pol.dense_row || qb >= pol.scored_rows)
+      dense_row(pol.Kb, cols, mrow, lane);
+    else
+      select_row(bsum + static_cast<int64_t>(qb) * pol.Kb, pol.n_cand, pol.k_pick, pol.dense_col, pol.Kb, cols,
+                 mrow, hist[w], lane);
+  }
+}
+
 struct TopkParams {
   const float* scores;  // [H][scored_rows][Kb]
   const int32_t* row_ptr;
@@ -849,19 +978,41 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 float* g_scratch[kMaxDevices] = {};
 
-// The current device's scratch address (hipGetSymbolAddress on the first call
-// on that device, with that device current).
-int scratch_for_current_device(const char* name, float** out) {
-  int dev = -1;
-  const hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+// Scratch address on the device that `stream` belongs to (the current device
+// for the null stream): the kernels run on that stream, so the scratch they
+// read must be that device's copy, whichever device is current. The address
+// is looked up once per device (hipGetSymbolAddress with that device made
+// current for the lookup, the caller's current device restored after).
+int scratch_for_stream(const char* name, hipStream_t stream, float** out) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) {
     set_error("%s: no usable current device (%s)", name, hipGetErrorString(e));
+    return 2;
+  }
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sd = -1;
+    e = hipStreamGetDevice(stream, &sd);
+    if (e != hipSuccess) {
+      set_error("%s: hipStreamGetDevice failed: %s", name, hipGetErrorString(e));
+      return 2;
+    }
+    dev = static_cast<int>(sd);
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: device %d out of range", name, dev);
     return 2;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (!g_scratch[dev]) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
+      set_error("%s: hipSetDevice(%d) failed: %s", name, dev, hipGetErrorString(e));
+      return 2;
+    }
     void* ptr = nullptr;
     const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
     if (rc != hipSuccess || !ptr) {
       set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev, hipGetErrorString(rc));
       return 2;
@@ -872,21 +1023,58 @@ int scratch_for_current_device(const char* name, float** out) {
   return 0;
 }
 
+// Tile sizes the scorer takes: 4..128 tokens, dividing the 128-token block.
+bool valid_tile(int64_t t) { return t >= 4 && t <= kBlock && kBlock % t == 0; }
+// Equal query and key tiles of 16 or 32 tokens run the tuned kernels (one
+// pass with a workspace); every other pair runs score_topk_tiles_kernel.
+bool tuned_tiles(int64_t q_tile, int64_t k_tile) { return q_tile == k_tile && (q_tile == 16 || q_tile == 32); }
+
 int score_topk_impl(const char* name, const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
                     const uint16_t* k_pool_hi, const uint16_t* k_pool_lo, int64_t heads, int64_t head_dim,
-                    int64_t tile_size, int64_t q_blocks, int64_t k_blocks, int64_t scored_rows, int64_t n_cand,
-                    int64_t k_pick, int64_t dense_col, int64_t dense_row, const int32_t* row_ptr,
-                    int32_t* col_idx, float* scores_out, uint8_t* mask_out, void* workspace,
+                    int64_t q_tile_size, int64_t k_tile_size, int64_t q_blocks, int64_t k_blocks,
+                    int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col, int64_t dense_row,
+                    const int32_t* row_ptr, int32_t* col_idx, float* scores_out, uint8_t* mask_out, void* workspace,
                     int64_t workspace_bytes, dfs_stream_t stream) {
   DFS_REQUIRE(q_pool_hi && q_pool_lo && k_pool_hi && k_pool_lo && row_ptr && col_idx,
               "%s: NULL operand", name);
   DFS_REQUIRE(head_dim == 64 || head_dim == 128, "%s: head_dim=%lld (supported: 64, 128)", name,
               (long long)head_dim);
-  DFS_REQUIRE(tile_size == 16 || tile_size == 32, "%s: tile_size=%lld (supported: 16, 32)", name,
-              (long long)tile_size);
+  DFS_REQUIRE(valid_tile(q_tile_size) && valid_tile(k_tile_size),
+              "%s: q_tile_size=%lld, k_tile_size=%lld (each must divide 128 and be at least 4)", name,
+              (long long)q_tile_size, (long long)k_tile_size);
   if (int rc = check_policy(name, heads, q_blocks, k_blocks, scored_rows, n_cand, k_pick,
                             dense_col, dense_row))
     return rc;
+  if (!tuned_tiles(q_tile_size, k_tile_size)) {
+    DFS_REQUIRE(scores_out != nullptr,
+                "%s: q_tile_size=%lld, k_tile_size=%lld run the generic scorer, which keeps its block sums "
+                "in scores_out: pass one", name, (long long)q_tile_size, (long long)k_tile_size);
+    ScoreParams p{};
+    p.q_hi = reinterpret_cast<const uint4*>(q_pool_hi);
+    p.q_lo = reinterpret_cast<const uint4*>(q_pool_lo);
+    p.k_hi = reinterpret_cast<const uint4*>(k_pool_hi);
+    p.k_lo = reinterpret_cast<const uint4*>(k_pool_lo);
+    p.row_ptr = row_ptr;
+    p.col_idx = col_idx;
+    p.scores_out = scores_out;
+    p.mask_out = mask_out;
+    p.pol = Policy{static_cast<int>(q_blocks), static_cast<int>(k_blocks), static_cast<int>(scored_rows),
+                   static_cast<int>(n_cand), static_cast<int>(k_pick), static_cast<int>(dense_col),
+                   static_cast<int>(dense_row)};
+    const int tpbq = static_cast<int>(kBlock / q_tile_size), tpbk = static_cast<int>(kBlock / k_tile_size);
+    p.q_tiles = static_cast<int>(scored_rows * tpbq);
+    p.k_tiles = static_cast<int>(k_blocks * tpbk);
+    p.scale_log2 = static_cast<float>(1.4426950408889634 / sqrt(static_cast<double>(head_dim)));
+    const int G = 4 * (32 / tpbq);  // query blocks per workgroup
+    const dim3 grid(static_cast<unsigned>((q_blocks + G - 1) / G), static_cast<unsigned>(heads));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (head_dim == 128)
+      score_topk_tiles_kernel<128><<<grid, 256, 0, s>>>(p, tpbq, tpbk);
+    else
+      score_topk_tiles_kernel<64><<<grid, 256, 0, s>>>(p, tpbq, tpbk);
+    return check_launch(name);
+  }
+  const int64_t tile_size = q_tile_size;
   const int tpb = static_cast<int>(kBlock / tile_size);
   const int G = 32 / tpb;
   const size_t smem = (static_cast<size_t>(G) * k_blocks + 512) * sizeof(float) + 4 * 256 * 4;
@@ -920,7 +1108,7 @@ int score_topk_impl(const char* name, const uint16_t* q_pool_hi, const uint16_t*
   // two-pass form.
   const int64_t row_cap = 32 * head_dim / 2;
   if (workspace && k_blocks <= row_cap) {
-    const int64_t need = dfs_block_score_topk_workspace_size(heads, tile_size, q_blocks, k_blocks);
+    const int64_t need = dfs_block_score_topk_workspace_size(heads, tile_size, tile_size, q_blocks, k_blocks);
     DFS_REQUIRE(workspace_bytes >= need, "%s: workspace of %lld bytes, %lld needed", name,
                 (long long)workspace_bytes, (long long)need);
     DFS_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15u) == 0, "%s: workspace must be 16-byte aligned",
@@ -979,9 +1167,12 @@ int score_topk_impl(const char* name, const uint16_t* q_pool_hi, const uint16_t*
 
 extern "C" {
 
-int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t tile_size, int64_t q_blocks,
-                                            int64_t k_blocks) {
-  if (heads <= 0 || q_blocks <= 0 || k_blocks <= 0 || (tile_size != 16 && tile_size != 32)) return -1;
+int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t q_tile_size, int64_t k_tile_size,
+                                            int64_t q_blocks, int64_t k_blocks) {
+  if (heads <= 0 || q_blocks <= 0 || k_blocks <= 0 || !dfs::valid_tile(q_tile_size) || !dfs::valid_tile(k_tile_size))
+    return -1;
+  if (!dfs::tuned_tiles(q_tile_size, k_tile_size)) return 0;  // no one-pass form for these tiles
+  const int64_t tile_size = q_tile_size;
   const int64_t tpb = dfs::kBlock / tile_size, Gw = 4 * (32 / tpb);
   const int64_t rows = (q_blocks + Gw - 1) / Gw * Gw * tpb;        // tile rows of every workgroup
   const int64_t cols = (k_blocks * tpb + 31) / 32 * (32 / tpb);  // key blocks of every 32-tile chunk
@@ -990,21 +1181,21 @@ int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t tile_size, in
 
 int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
                          const uint16_t* k_pool_hi, const uint16_t* k_pool_lo, int64_t heads,
-                         int64_t head_dim, int64_t tile_size, int64_t q_blocks, int64_t k_blocks,
-                         int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
+                         int64_t head_dim, int64_t q_tile_size, int64_t k_tile_size, int64_t q_blocks,
+                         int64_t k_blocks, int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
                          int64_t dense_row, const int32_t* row_ptr, int32_t* col_idx,
                          float* scores_out, uint8_t* mask_out, void* workspace, int64_t workspace_bytes,
                          dfs_stream_t stream) {
   return dfs::score_topk_impl("dfs_block_score_topk", q_pool_hi, q_pool_lo, k_pool_hi, k_pool_lo, heads, head_dim,
-                              tile_size, q_blocks, k_blocks, scored_rows, n_cand, k_pick, dense_col, dense_row,
-                              row_ptr, col_idx, scores_out, mask_out, workspace, workspace_bytes, stream);
+                              q_tile_size, k_tile_size, q_blocks, k_blocks, scored_rows, n_cand, k_pick, dense_col,
+                              dense_row, row_ptr, col_idx, scores_out, mask_out, workspace, workspace_bytes, stream);
 }
 
 int dfs_block_score_topk_noalloc(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
                                  const uint16_t* k_pool_hi, const uint16_t* k_pool_lo, int64_t heads,
-                                 int64_t head_dim, int64_t tile_size, int64_t q_blocks, int64_t k_blocks,
-                                 int64_t scored_rows, int64_t n_cand, int64_t k_pick, int64_t dense_col,
-                                 int64_t dense_row, const int32_t* row_ptr, int32_t* col_idx,
+                                 int64_t head_dim, int64_t q_tile_size, int64_t k_tile_size, int64_t q_blocks,
+                                 int64_t k_blocks, int64_t scored_rows, int64_t n_cand, int64_t k_pick,
+                                 int64_t dense_col, int64_t dense_row, const int32_t* row_ptr, int32_t* col_idx,
                                  uint8_t* mask_out, dfs_stream_t stream) {
   using namespace dfs;
   const char* name = "dfs_block_score_topk_noalloc";
@@ -1016,12 +1207,12 @@ int dfs_block_score_topk_noalloc(const uint16_t* q_pool_hi, const uint16_t* q_po
               name, (long long)heads, (long long)scored_rows, (long long)k_blocks, (long long)need,
               (long long)kScratchBytes);
   float* sums = nullptr;
-  if (int rc = scratch_for_current_device(name, &sums)) return rc;
+  if (int rc = scratch_for_stream(name, reinterpret_cast<hipStream_t>(stream), &sums)) return rc;
   // Two-pass form: the block sums are the only scratch (every entry is
   // written by the kernel, so nothing needs clearing between calls).
-  return score_topk_impl(name, q_pool_hi, q_pool_lo, k_pool_hi, k_pool_lo, heads, head_dim, tile_size, q_blocks,
-                         k_blocks, scored_rows, n_cand, k_pick, dense_col, dense_row, row_ptr, col_idx, sums,
-                         mask_out, nullptr, 0, stream);
+  return score_topk_impl(name, q_pool_hi, q_pool_lo, k_pool_hi, k_pool_lo, heads, head_dim, q_tile_size,
+                         k_tile_size, q_blocks, k_blocks, scored_rows, n_cand, k_pick, dense_col, dense_row, row_ptr,
+                         col_idx, sums, mask_out, nullptr, 0, stream);
 }
 
 int dfs_topk_from_scores(const float* scores, int64_t heads, int64_t q_blocks, int64_t k_blocks,

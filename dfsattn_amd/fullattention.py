@@ -7,7 +7,8 @@
 * ``"flash"`` (varlen semantics of ``flash_attn_varlen_func``): query
   segment i of ``cu_seqlens_q`` attends key segment i of ``cu_seqlens_kv``.
   Self-attention (bf16/f16 on the GPU) runs on this library's block-sparse
-  kernel with every block kept, the segment split read on the device.
+  kernel with every block kept, the segment split read on the device (host
+  cu_seqlens of more than two segments run one segment per call).
   Rectangular attention (cross-attention, e.g. Wan's 512 text tokens) runs on
   torch's ``scaled_dot_product_attention``, with a segment mask built on the
   device when device cu_seqlens are given. Host cu_seqlens are read on the
@@ -117,7 +118,11 @@ def _flash(q, k, v, cu_seqlens_q, cu_seqlens_kv, batch_size, operand_dtype=None)
     sk = k.shape[2]
     on_host = all(c is None or c.device.type == "cpu" for c in (cu_seqlens_q, cu_seqlens_kv))
     native = q.is_cuda and q.dtype in (torch.bfloat16, torch.float16) and sq == sk
-    if q.is_cuda and (native or not on_host):
+    # The device varlen path takes at most two sequences; host splits into
+    # more run segment by segment below (each square segment on the native
+    # kernel).
+    many = on_host and any(c is not None and c.numel() > 3 for c in (cu_seqlens_q, cu_seqlens_kv))
+    if q.is_cuda and (native or not on_host) and not many:
         # Device path: the segment split stays on the device.
         cq = _device_cu(cu_seqlens_q, sq, q.device)
         ck = _device_cu(cu_seqlens_kv, sk, q.device)
@@ -152,7 +157,10 @@ def _flash(q, k, v, cu_seqlens_q, cu_seqlens_kv, batch_size, operand_dtype=None)
                 continue  # no queries, or no keys: the reference kernel writes zeros
             qs, ks, vs = (x[bi:bi + 1, :, r0:r1].contiguous()
                           for x, (r0, r1) in ((q, (q0, q1)), (k, (k0, k1)), (v, (k0, k1))))
-            out[bi:bi + 1, :, q0:q1] = _sdpa(qs, ks, vs)
+            if native and q1 - q0 == k1 - k0:
+                out[bi:bi + 1, :, q0:q1] = dense_attention_native(qs, ks, vs, operand_dtype=operand_dtype)
+            else:
+                out[bi:bi + 1, :, q0:q1] = _sdpa(qs, ks, vs)
     return out
 
 

@@ -9,10 +9,13 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
+from typing import Optional
 
 import numpy as np
 
 BLOCK = 128
+# Smallest tile the scoring kernel takes (32 tiles per 128-token block).
+MIN_TILE = 4
 
 
 @dataclass(frozen=True)
@@ -26,15 +29,27 @@ class ScoringLayout:
 
     seq_len: int
     video_len: int
-    tile: int
+    tile: int  # query tile (q_tile_size)
     block: int = BLOCK
+    k_tile: Optional[int] = None  # key tile (k_tile_size); None: the query tile
 
     def __post_init__(self):
+        if self.k_tile is None:
+            object.__setattr__(self, "k_tile", self.tile)
         if self.block != BLOCK:
             raise ValueError(f"native DFS execution requires block_size == {BLOCK}, got {self.block}")
-        if self.block % self.tile != 0:
+        # attention_wan.py:227-228; attention_hyvideo.py:406-407
+        if self.tile <= 0 or self.block % self.tile != 0:
             raise AssertionError(
                 f"block_dim ({self.block}) must be divisible by q_tile_size ({self.tile})")
+        if self.k_tile <= 0 or self.block % self.k_tile != 0:
+            raise AssertionError(
+                f"block_dim ({self.block}) must be divisible by k_tile_size ({self.k_tile})")
+        for name, t in (("q_tile_size", self.tile), ("k_tile_size", self.k_tile)):
+            if t < MIN_TILE:
+                raise NotImplementedError(
+                    f"{name} {t}: the scoring kernel takes tiles of {MIN_TILE} to {self.block} tokens "
+                    f"(at most {self.block // MIN_TILE} tiles per block)")
         if not 0 < self.video_len <= self.seq_len:
             raise ValueError(f"need 0 < video_len ({self.video_len}) <= seq_len ({self.seq_len})")
         padded = self.video_blocks * self.block + self.text_len
@@ -64,12 +79,16 @@ class ScoringLayout:
         return math.ceil(self.video_len / self.block)
 
     @property
+    def q_tile(self) -> int:
+        return self.tile
+
+    @property
     def q_tiles(self) -> int:
         return self.video_blocks * self.block // self.tile
 
     @property
     def k_tiles(self) -> int:
-        return self.k_blocks * self.block // self.tile
+        return self.k_blocks * self.block // self.k_tile
 
 
 @dataclass(frozen=True)

@@ -167,7 +167,7 @@ def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.T
     rounds = q.dtype == torch.bfloat16 and operand_dtype == torch.float16
     flags = torch.zeros(3 * heads, dtype=torch.int32, device=dev) if rounds else None
     _lib.call("dfs_prepare_qkv", _ptr(q), _ptr(k), _ptr(v), _ptr(perm), heads, length, dim,
-              DTYPE_CODE[q.dtype], layout.video_len, layout.tile, DTYPE_CODE[operand_dtype],
+              DTYPE_CODE[q.dtype], layout.video_len, layout.q_tile, layout.k_tile, DTYPE_CODE[operand_dtype],
               _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(prep.q_hi), _ptr(prep.q_lo),
               _ptr(prep.k_hi), _ptr(prep.k_lo), _ptr(flags), _stream(q))
     if rounds:
@@ -182,11 +182,14 @@ def _policy_args(policy: TopkPolicy):
             policy.dense_col, policy.dense_row)
 
 
-def score_workspace_bytes(heads: int, tile: int, q_blocks: int, k_blocks: int) -> int:
-    """Bytes of the one-pass scoring workspace (per-tile partial block sums)."""
-    n = int(_lib.lib().dfs_block_score_topk_workspace_size(heads, tile, q_blocks, k_blocks))
+def score_workspace_bytes(heads: int, q_tile: int, k_tile: int, q_blocks: int, k_blocks: int) -> int:
+    """Bytes of the one-pass scoring workspace (per-tile partial block sums);
+    0 when these tile sizes have no one-pass form (the scorer then runs its
+    two passes)."""
+    n = int(_lib.lib().dfs_block_score_topk_workspace_size(heads, q_tile, k_tile, q_blocks, k_blocks))
     if n < 0:
-        raise ValueError(f"no scoring workspace for heads={heads} tile={tile} blocks={q_blocks}x{k_blocks}")
+        raise ValueError(f"no scoring workspace for heads={heads} tiles={q_tile}/{k_tile} "
+                         f"blocks={q_blocks}x{k_blocks}")
     return n
 
 
@@ -209,17 +212,18 @@ def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
     dev = prep.q_perm.device
     nnz = policy.nnz(prep.heads)
     col_idx = torch.empty(nnz, dtype=torch.int32, device=dev)
-    one_pass_rows = one_pass and policy.k_blocks <= 16 * prep.head_dim
+    q_tile, k_tile = prep.layout.q_tile, prep.layout.k_tile
+    ws_bytes = 0
+    if one_pass and policy.k_blocks <= 16 * prep.head_dim:
+        ws_bytes = score_workspace_bytes(prep.heads, q_tile, k_tile, policy.q_blocks, policy.k_blocks)
+    one_pass_rows = ws_bytes > 0
     scores = (torch.empty((prep.heads, policy.scored_rows, policy.k_blocks), dtype=torch.float32, device=dev)
               if want_scores or not one_pass_rows else None)
     mask = (torch.empty((prep.heads, policy.q_blocks, policy.k_blocks), dtype=torch.uint8, device=dev)
             if want_mask else None)
-    ws, ws_bytes = None, 0
-    if one_pass_rows:
-        ws_bytes = score_workspace_bytes(prep.heads, prep.layout.tile, policy.q_blocks, policy.k_blocks)
-        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev)
+    ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev) if one_pass_rows else None
     _lib.call("dfs_block_score_topk", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi), _ptr(prep.k_lo),
-              prep.heads, prep.head_dim, prep.layout.tile, *_policy_args(policy), _ptr(row_ptr),
+              prep.heads, prep.head_dim, q_tile, k_tile, *_policy_args(policy), _ptr(row_ptr),
               _ptr(col_idx), _ptr(scores), _ptr(mask), _ptr(ws), ws_bytes, _stream(prep.q_perm))
     return col_idx, (scores if want_scores else None), mask
 
@@ -240,9 +244,13 @@ def block_score_topk_noalloc(prep: Prepared, policy: TopkPolicy, row_ptr: torch.
     col_idx = torch.empty(policy.nnz(prep.heads), dtype=torch.int32, device=dev)
     mask = (torch.empty((prep.heads, policy.q_blocks, policy.k_blocks), dtype=torch.uint8, device=dev)
             if want_mask else None)
-    _lib.call("dfs_block_score_topk_noalloc", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi), _ptr(prep.k_lo),
-              prep.heads, prep.head_dim, prep.layout.tile, *_policy_args(policy), _ptr(row_ptr), _ptr(col_idx),
-              _ptr(mask), _stream(prep.q_perm))
+    # The library takes its scratch from the stream's device; the tensors'
+    # device is also made current so that the launch and the stream agree
+    # whichever device the caller has current.
+    with torch.cuda.device(dev):
+        _lib.call("dfs_block_score_topk_noalloc", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi),
+                  _ptr(prep.k_lo), prep.heads, prep.head_dim, prep.layout.q_tile, prep.layout.k_tile,
+                  *_policy_args(policy), _ptr(row_ptr), _ptr(col_idx), _ptr(mask), _stream(prep.q_perm))
     return col_idx, mask
 
 

@@ -40,7 +40,8 @@ enum { DFS_DTYPE_BF16 = 0, DFS_DTYPE_F16 = 1, DFS_DTYPE_F32 = 2 };
 const char* dfs_last_error(void);
 
 /* ABI version; bumped whenever a signature below changes (2: scoring workspace; 3: device cu_seqlens
- * and per-head operand exponents in the attention call, per-head overflow flags and dfs_prepare_fixup). */
+ * and per-head operand exponents in the attention call, per-head overflow flags and dfs_prepare_fixup;
+ * 4: separate query and key tile sizes in preparation and scoring). */
 int dfs_abi_version(void);
 
 /*
@@ -76,7 +77,9 @@ int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst,
 
 /*
  * Fused permute of Q, K, V into the attention operand layouts plus mean
- * pooling of Q and K over tile_size-token tiles in the scoring layout.
+ * pooling of Q over q_tile_size-token tiles and of K over k_tile_size-token
+ * tiles in the scoring layout (each a divisor of 128; the reference's
+ * q_tile_size / k_tile_size, attention_wan.py:94-95, 192-205).
  *   dtype        0 (bf16) or 1 (f16) for the inputs q, k, v.
  *   video_len    L for Wan; the video token count for HunyuanVideo. The
  *                scoring layout is [video | zero pad to 128 | text | zero
@@ -85,8 +88,9 @@ int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst,
  *   operand_dtype  dtype of q_perm, k_perm and v_t: 0 keeps the bf16 bits
  *                (bf16 inputs only); 1 holds f16 (bf16 inputs are rounded
  *                to f16, exact for values inside the f16 range).
- *   q_pool_*     [H][ceil(video_len/128)*128/tile][D] (may all be NULL to skip
- *   k_pool_*     [H][ceil(L/128)*128/tile][D]          pooling: cached steps).
+ *   q_pool_*     [H][ceil(video_len/128)*128/q_tile_size][D] (may all be
+ *   k_pool_*     [H][ceil(L/128)*128/k_tile_size][D]  NULL to skip pooling:
+ *                cached steps).
  *                Means of the input values, whatever operand_dtype.
  *   overflow     optional int32 [3][H] flags (Q, K, V per head), zeroed by
  *                the caller; entry [t][h] is set when bf16 inputs are
@@ -98,7 +102,7 @@ int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst,
 int dfs_prepare_qkv(const void* q, const void* k, const void* v,
                     const int32_t* perm, int64_t heads, int64_t seq_len,
                     int64_t head_dim, int dtype, int64_t video_len,
-                    int64_t tile_size, int operand_dtype,
+                    int64_t q_tile_size, int64_t k_tile_size, int operand_dtype,
                     void* q_perm, void* k_perm, void* v_t,
                     uint16_t* q_pool_hi, uint16_t* q_pool_lo,
                     uint16_t* k_pool_hi, uint16_t* k_pool_lo,
@@ -124,6 +128,11 @@ int dfs_prepare_fixup(const void* q, const void* k, const void* v,
  * Hierarchical block scoring and top-k in one kernel: pooled QK^T * D^-1/2
  * (bf16 MFMA on the hi/lo split), softmax over all key tiles, sums of tile
  * probabilities per 128x128 block, then per-row top-k.
+ *   q_tile_size, k_tile_size  tokens per pooled query / key tile, each a
+ *                divisor of 128 of at least 4, as pooled by dfs_prepare_qkv
+ *                (attention_wan.py:94-95, 227-246). Equal tiles of 16 or 32
+ *                run the tuned kernels; any other pair runs a generic
+ *                two-pass kernel that needs scores_out.
  * Row selection policy (same as dfs_topk_from_scores):
  *   scored_rows  number of query-block rows that carry scores
  *                (ceil(video_len/128)).
@@ -149,7 +158,8 @@ int dfs_prepare_fixup(const void* q, const void* k, const void* v,
  */
 int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
                          const uint16_t* k_pool_hi, const uint16_t* k_pool_lo,
-                         int64_t heads, int64_t head_dim, int64_t tile_size,
+                         int64_t heads, int64_t head_dim,
+                         int64_t q_tile_size, int64_t k_tile_size,
                          int64_t q_blocks, int64_t k_blocks,
                          int64_t scored_rows, int64_t n_cand, int64_t k_pick,
                          int64_t dense_col, int64_t dense_row,
@@ -160,29 +170,33 @@ int dfs_block_score_topk(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
 
 /*
  * Bytes of the optional dfs_block_score_topk workspace for these sizes
- * (-1 for invalid sizes). Host function; no reference counterpart (the
- * reference materialises the whole [H, Qt, Kt] tile-score tensor instead,
- * attention_wan.py:207-209).
+ * (-1 for invalid sizes, 0 for tile sizes without a one-pass form). Host
+ * function; no reference counterpart (the reference materialises the whole
+ * [H, Qt, Kt] tile-score tensor instead, attention_wan.py:207-209).
  */
-int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t tile_size,
-                                            int64_t q_blocks, int64_t k_blocks);
+int64_t dfs_block_score_topk_workspace_size(int64_t heads, int64_t q_tile_size,
+                                            int64_t k_tile_size, int64_t q_blocks,
+                                            int64_t k_blocks);
 
 /*
  * dfs_block_score_topk that allocates nothing and takes no caller scratch:
  * the block-sum matrix (heads * scored_rows * k_blocks fp32 values, at most
  * 96 MiB: 55.9 MB at 75.6k tokens x 40 heads, 83.0 MB at 119k tokens x 24
  * heads) lives in a static device array of the library, one per GPU, held
- * until the process ends; larger problems are rejected with an error. Runs
- * the two-pass form (no workspace); same selection as dfs_block_score_topk
- * with scores_out and no workspace. Calls that overlap on one GPU (several
- * streams or threads) share that array and race; serialise them. No
+ * until the process ends; larger problems are rejected with an error. The
+ * copy used is that of the device `stream` belongs to (the current device
+ * for the null stream), whichever device is current. Runs the two-pass form
+ * (no workspace); same selection as dfs_block_score_topk with scores_out and
+ * no workspace. Calls that overlap on one GPU (several streams or threads)
+ * share that array and race; serialise them. No
  * counterpart in the reference: it is for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).
  */
 int dfs_block_score_topk_noalloc(const uint16_t* q_pool_hi, const uint16_t* q_pool_lo,
                                  const uint16_t* k_pool_hi, const uint16_t* k_pool_lo,
-                                 int64_t heads, int64_t head_dim, int64_t tile_size,
+                                 int64_t heads, int64_t head_dim,
+                                 int64_t q_tile_size, int64_t k_tile_size,
                                  int64_t q_blocks, int64_t k_blocks,
                                  int64_t scored_rows, int64_t n_cand, int64_t k_pick,
                                  int64_t dense_col, int64_t dense_row,

@@ -14,18 +14,22 @@ Each function restates the reference (``codesiena/DFSattn``) at the cited
   closed forms (1 bit per axis = inverse Gray code of the interleaved
   coordinate bits, axis 0 most significant), the Hilbert-curve invariants
   (bijection, unit steps on full 2^b cubes, index 0 at the origin), the
-  package's published usage example (2-D, 3 bits), a round trip through a
-  separate restatement of the package's ``decode`` (which fails for the
-  encoder's loops in another order or without the exchange step) and an
-  independent C implementation. The exact numpy-hilbert-curve bit convention
-  beyond these is **parity unpinned** (the package is absent offline and the
-  reference ships no fixture for it).
+  package's published usage example (2-D, 3 bits: it fixes the axis order at
+  the finest level), a round trip through a separate restatement of the
+  package's ``decode`` on full cubes and on 3-D 7-bit points (an encoder with
+  its bit or axis loops reversed, its axes swapped, the exchange step dropped
+  or the inversion on the wrong axis fails it) and an independent C
+  implementation on the benchmark grids. Together these fix the package's
+  convention: every plausible variant of the encoder that was tried fails one
+  of them. No fixture of the package's own output exists (it is absent
+  offline and the reference ships none), so that is the anchor.
 * ``compute_cache_schedule`` (dfsattn/attention_wan.py:41-66): pinned by the
   reference's own known-answer test (tests/test_flashinfer64_attention.py:122-157).
 * ``tile_scores`` / ``block_scores`` (attention_wan.py:157-246,
-  attention_hyvideo.py:310-422): pinned by a brute-force loop restatement on
-  tiny inputs and the invariant that every scored row of block scores sums to
-  block/tile (softmax rows sum to one).
+  attention_hyvideo.py:310-422), with equal or unequal query and key tiles:
+  pinned by a brute-force loop restatement on tiny inputs and the invariant
+  that every scored row of block scores sums to block/q_tile (softmax rows
+  sum to one).
 * ``mask_from_scores_*`` (attention_wan.py:248-253, attention_hyvideo.py:424-501):
   pinned against ``torch.topk`` + ``scatter_`` (the reference's own calls) on
   tie-free scores, and by policy invariants (row counts, dense text columns/rows).
@@ -326,10 +330,19 @@ def _scoring_layout(x_perm: torch.Tensor, seq_len: int, video_len: int, block: i
     return out
 
 
+def _check_tiles(block: int, q_tile: int, k_tile: int) -> None:
+    """attention_wan.py:227-228; attention_hyvideo.py:406-407."""
+    assert block % q_tile == 0, f"block_dim ({block}) must be divisible by q_tile_size ({q_tile})"
+    assert block % k_tile == 0, f"block_dim ({block}) must be divisible by k_tile_size ({k_tile})"
+
+
 def pooled_tiles(q_perm: torch.Tensor, k_perm: torch.Tensor, tile: int, block: int = BLOCK,
-                 video_len: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Tile means of the scoring layout: queries over the video part, keys over
-    everything (attention_wan.py:192-205; attention_hyvideo.py:367-381)."""
+                 video_len: Optional[int] = None, k_tile: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Tile means of the scoring layout: queries over the video part in
+    ``tile``-token tiles, keys over everything in ``k_tile``-token tiles
+    (default: ``tile``) (attention_wan.py:192-205; attention_hyvideo.py:367-381)."""
+    k_tile = tile if k_tile is None else k_tile
+    _check_tiles(block, tile, k_tile)
     seq_len = q_perm.shape[2]
     video_len = seq_len if video_len is None else video_len
     qs = _scoring_layout(q_perm.float(), seq_len, video_len, block)
@@ -337,31 +350,34 @@ def pooled_tiles(q_perm: torch.Tensor, k_perm: torch.Tensor, tile: int, block: i
     bsz, heads, _, dim = qs.shape
     vpad_len = math.ceil(video_len / block) * block
     qt = qs[:, :, :vpad_len].reshape(bsz, heads, vpad_len // tile, tile, dim).mean(dim=3)
-    kt = ks.reshape(bsz, heads, ks.shape[2] // tile, tile, dim).mean(dim=3)
+    kt = ks.reshape(bsz, heads, ks.shape[2] // k_tile, k_tile, dim).mean(dim=3)
     return qt, kt
 
 
 def tile_scores(q_perm: torch.Tensor, k_perm: torch.Tensor, tile: int, block: int = BLOCK,
-                video_len: Optional[int] = None) -> torch.Tensor:
+                video_len: Optional[int] = None, k_tile: Optional[int] = None) -> torch.Tensor:
     """fp32 softmax(Qt Kt^T / sqrt(D)) over all key tiles, [B, H, Qt, Kt]
     (attention_wan.py:207; attention_hyvideo.py:383)."""
-    qt, kt = pooled_tiles(q_perm, k_perm, tile, block, video_len)
+    qt, kt = pooled_tiles(q_perm, k_perm, tile, block, video_len, k_tile)
     scale = 1.0 / math.sqrt(q_perm.shape[-1])
     return (qt @ kt.transpose(-2, -1) * scale).softmax(dim=-1)
 
 
 def block_scores(q_perm: torch.Tensor, k_perm: torch.Tensor, tile: int, block: int = BLOCK,
-                 video_len: Optional[int] = None, head_chunk: int = 4) -> torch.Tensor:
-    """Block sums of tile probabilities, fp32 [H, Vb, Kb]
+                 video_len: Optional[int] = None, head_chunk: int = 4, k_tile: Optional[int] = None) -> torch.Tensor:
+    """Block sums of tile probabilities, fp32 [H, Vb, Kb]: the sum over a
+    block's block/tile query tiles and block/k_tile key tiles
     (attention_wan.py:243-246; attention_hyvideo.py:419-422), computed a few
     heads at a time to bound memory at the full configurations."""
     heads = q_perm.shape[1]
-    tpb = block // tile
+    k_tile = tile if k_tile is None else k_tile
+    tpq, tpk = block // tile, block // k_tile
     outs = []
     for h0 in range(0, heads, head_chunk):
-        ts = tile_scores(q_perm[:, h0:h0 + head_chunk], k_perm[:, h0:h0 + head_chunk], tile, block, video_len)
+        ts = tile_scores(q_perm[:, h0:h0 + head_chunk], k_perm[:, h0:h0 + head_chunk], tile, block, video_len,
+                         k_tile)
         b, hh, qt, kt = ts.shape
-        outs.append(ts.view(b, hh, qt // tpb, tpb, kt // tpb, tpb).sum(dim=(3, 5))[0])
+        outs.append(ts.view(b, hh, qt // tpq, tpq, kt // tpk, tpk).sum(dim=(3, 5))[0])
     return torch.cat(outs, dim=0)
 
 
@@ -526,7 +542,8 @@ def expand_block_mask(mask: torch.Tensor, seq_len: int, block: int = BLOCK) -> t
 
 def dfs_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, video_perm: torch.Tensor,
                             sparse_ratio: float, tile: int, block: int = BLOCK,
-                            video_len: Optional[int] = None, valid: Optional[int] = None):
+                            video_len: Optional[int] = None, valid: Optional[int] = None,
+                            k_tile: Optional[int] = None):
     """Permute, score, select, attend, unpermute. Returns (out fp32 [1,H,L,D]
     in the original order, bool mask [H,Qb,Kb], fp32 block scores). With
     ``valid`` < L (cu_seqlens [0, valid, L]) the mask is still selected over
@@ -534,7 +551,7 @@ def dfs_attention_reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, v
     seq_len = q.shape[2]
     perm, inv = full_permutation(video_perm, seq_len)
     qp, kp, vp = apply_permutation(q, perm), apply_permutation(k, perm), apply_permutation(v, perm)
-    scores = block_scores(qp, kp, tile, block, video_len)
+    scores = block_scores(qp, kp, tile, block, video_len, k_tile=k_tile)
     if video_len is None:
         mask = mask_from_scores_wan(scores, sparse_ratio)
     else:

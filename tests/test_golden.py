@@ -117,7 +117,7 @@ def test_gpu_matches_fixture(name, dev):
     prep = ops.prepare_qkv(q, k, v, perm_d, lay)
     # scoring: fp32 block scores of the GPU against the fixture
     _, scores, _ = ops.block_score_topk(prep, pol, row_ptr, want_scores=True)
-    np.testing.assert_allclose(scores.cpu().numpy(), g["scores"], rtol=2e-3, atol=1e-5)
+    np.testing.assert_allclose(scores.cpu().numpy(), g["scores"], rtol=1e-5, atol=1e-10)
     # selection from the fixture's own fp32 scores: bit-exact mask
     col_idx, mask = ops.topk_from_scores(torch.from_numpy(g["scores"]).to(dev), pol, row_ptr, want_mask=True)
     assert np.array_equal(mask.cpu().numpy().astype(bool), g["mask"])

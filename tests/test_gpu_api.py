@@ -419,3 +419,46 @@ def test_bf16_operand_setting_through_the_call(dev):
     assert _rel(out.cpu(), ref) < 5e-3 and float((out.cpu().float() - ref).abs().max()) < 2e-2
     ref_dense = orc.dense_attention(q.float(), k.float(), v.float())
     assert _rel(dense.cpu(), ref_dense) < 5e-3
+
+
+@pytest.mark.parametrize("variant,q_tile,k_tile", [("wan", 8, 64), ("wan", 128, 32), ("hunyuan", 64, 16),
+                                                   ("hunyuan", 32, 4)])
+def test_dfs_attention_class_with_unequal_tiles(dev, variant, q_tile, k_tile):
+    """DFS_Attention with separate q_tile_size / k_tile_size (the class
+    arguments, attention_wan.py:94-95, 192-203; attention_hyvideo.py:125-126):
+    the cached mask is the oracle's selection over the GPU's fp32 scores, and
+    the output matches the oracle's whole call."""
+    from dfsattn_amd import ops
+    from dfsattn_amd.layout import ScoringLayout, hunyuan_policy, wan_policy
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+
+    text = 100 if variant == "hunyuan" else 0
+    cfg = DfsConfig("t", (4, 16, 40), 2, 128, torch.bfloat16, text_len=text, seed=31)  # 2,560 video tokens
+    q, k, v = synth_qkv(cfg)
+    L, video = cfg.seq_len, cfg.video_len
+    perm = torch.randperm(video, generator=torch.Generator().manual_seed(32))
+    if variant == "wan":
+        from dfsattn_amd.attention_wan import DFS_Attention
+        att = DFS_Attention(step_idx=0, layer_idx=7, sparse_ratio=0.3, cache_flag=True, video_perm=perm,
+                            q_tile_size=q_tile, k_tile_size=k_tile)
+    else:
+        from dfsattn_amd.attention_hyvideo import DFS_Attention
+        att = DFS_Attention(step_idx=0, layer_idx=7, sparse_ratio=0.3, cache_flag=True, video_perm=perm,
+                            video_len=video, q_tile_size=q_tile, k_tile_size=k_tile)
+    out = att.forward(q.to(dev), k.to(dev), v.to(dev))
+    ref, _, ref_scores = orc.dfs_attention_reference(q.float(), k.float(), v.float(), perm, 0.3, q_tile,
+                                                     video_len=video if text else None, k_tile=k_tile)
+    entry = next(iter(type(att)._cached_metadata.values()))
+    mask = entry["block_mask"].cpu()
+    # the GPU's own scores for this call, and the selection rule over them
+    lay = ScoringLayout(L, video, q_tile, k_tile=k_tile)
+    pol = hunyuan_policy(lay, 0.3) if text else wan_policy(lay, 0.3)
+    full, inv = orc.full_permutation(perm, L)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ops.device_perm(full, dev), lay)
+    _, scores, _ = ops.block_score_topk(prep, pol, torch.from_numpy(pol.row_ptr(2)).to(dev), want_scores=True)
+    got = scores.cpu()
+    assert torch.allclose(got, ref_scores, rtol=1e-5, atol=1e-10)
+    sel = (orc.mask_from_scores_hunyuan(got, 0.3, L, video) if text else orc.mask_from_scores_wan(got, 0.3))
+    assert torch.equal(mask, sel)
+    ref_own = orc.masked_attention(*(orc.apply_permutation(x.float(), full) for x in (q, k, v)), mask)[:, :, inv]
+    assert _rel(out.cpu(), ref_own) < 4e-3 and float((out.cpu().float() - ref_own).abs().max()) < 2e-2

@@ -3,7 +3,8 @@ sequential denoising calls with Q_t = Q_{t-1} + N(0, 0.02) (likewise K):
 the first 12 real steps dense, then dfs_attention with skip 12, interval 12
 and the step counter counting CFG passes (attention_wan.py:41-66, 432-470,
 792-800). Checks the refresh steps and their top-k sizes for sparsity 0.3
-with the reference's default decay 0.1 and without decay, that cached calls
+with the reference's default decay 0.1 and without decay, and for sparsity
+0.5 (the sweep's largest point) without decay, that cached calls
 reuse the refreshed columns bit for bit, the fresh selection (bit-exact
 from the GPU's own fp32 scores, and against the oracle's fp32 scores up to
 near-ties), and sampled query blocks of one refresh call and one
@@ -72,9 +73,10 @@ def _check_selection(dev, entry, q, k, v, full, perm_d, lay, kpick, label):
     assert all(g <= 2 * err for g in gaps), (gaps, err)
 
 
-@pytest.mark.parametrize("dcrt,expect", [(0.1, {12: 177, 24: 118, 36: 59}),
-                                         (0.0, {12: 177, 24: 177, 36: 177, 48: 177})])
-def test_mask_cache_regime_at_cfg1_shape(dev, dcrt, expect):
+@pytest.mark.parametrize("sparsity,dcrt,expect", [(0.3, 0.1, {12: 177, 24: 118, 36: 59}),
+                                                  (0.3, 0.0, {12: 177, 24: 177, 36: 177, 48: 177}),
+                                                  (0.5, 0.0, {12: 295, 24: 295, 36: 295, 48: 295})])
+def test_mask_cache_regime_at_cfg1_shape(dev, sparsity, dcrt, expect):
     from dfsattn_amd import ops
     from dfsattn_amd.attention_wan import DFS_Attention, _dfs_attention_instances, dfs_attention
     from dfsattn_amd.fullattention import full_attention
@@ -104,22 +106,23 @@ def test_mask_cache_regime_at_cfg1_shape(dev, dcrt, expect):
                 assert bool(torch.isfinite(dense).all())
             continue
         out = dfs_attention(q, k, v, step_idx=2 * t, skip_steps=12, cache_interval=12, layer_idx=0,
-                            sparsity=0.3, sparsity_dcrt=dcrt, tile_size=cfg.tile, video_perm=perm, cache_flag=True)
+                            sparsity=sparsity, sparsity_dcrt=dcrt, tile_size=cfg.tile, video_perm=perm,
+                            cache_flag=True)
         entry = DFS_Attention._cached_metadata[key]
         if entry is not prev:  # a refresh stored a new entry
             kpick = int((entry["row_ptr"][1] - entry["row_ptr"][0]).item())
             refreshes[t] = kpick
             kept_cols = entry["col_idx"].clone()
             if t == 24:  # the fresh selection of head 0 against the oracle's fp32 scores
-                _check_selection(dev, entry, q, k, v, full, perm_d, lay, kpick, f"dcrt {dcrt} step {t}")
+                _check_selection(dev, entry, q, k, v, full, perm_d, lay, kpick, f"s {sparsity} dcrt {dcrt} step {t}")
             if t == 12:
-                _check_output(dev, entry, q, k, v, full, perm_d, lay, out, f"dcrt {dcrt} refresh step {t}")
+                _check_output(dev, entry, q, k, v, full, perm_d, lay, out, f"s {sparsity} dcrt {dcrt} refresh step {t}")
         else:
             assert torch.equal(entry["col_idx"], kept_cols)  # the cached columns, bit for bit
             if t == 13:
-                _check_output(dev, entry, q, k, v, full, perm_d, lay, out, f"dcrt {dcrt} cached step {t}")
+                _check_output(dev, entry, q, k, v, full, perm_d, lay, out, f"s {sparsity} dcrt {dcrt} cached step {t}")
         prev = entry
-    print(f"dcrt {dcrt}: refreshes at real steps {refreshes}", flush=True)
+    print(f"s {sparsity} dcrt {dcrt}: refreshes at real steps {refreshes}", flush=True)
     assert refreshes == expect
     DFS_Attention.clear_cache()
     _dfs_attention_instances.clear()

@@ -1,9 +1,10 @@
 """Full-size parity at the benchmark shapes (configs[1] Wan, configs[2]
 HunyuanVideo) through properties that do not need a full CPU reference:
 per-row kept-block counts and the policy's dense rows/columns over every
-head, fp32 block scores of one head against the oracle, the selection
-bit-exact from the GPU's own fp32 scores, and sampled query blocks of the
-output against fp32 masked attention on the host."""
+head, fp32 block scores of two heads against the oracle, the selection
+bit-exact from the GPU's own fp32 scores and near-tie-only differences from
+the oracle's, and eight query blocks of four heads (HunyuanVideo's dense text
+rows included) against fp32 masked attention on the host."""
 import pytest
 import torch
 
@@ -54,43 +55,50 @@ def test_full_size_call(dev, cfg_id):
         assert bool((counts == topk_count(cfg.sparsity, kb)).all())
     assert bool((mask.sum(-1) == counts).all())
 
-    # scores of head 0 against the oracle; selection exact from the GPU's own scores
+    # scores of the first and last heads against the oracle; the selection is
+    # exact from the GPU's own scores
     full, _ = orc.full_permutation(perm, L)
     perm_d = ops.device_perm(full, dev)
-    prep = ops.prepare_qkv(q[:, :1], k[:, :1], v[:, :1], perm_d, lay)
-    row_ptr1 = torch.from_numpy(pol.row_ptr(1)).to(dev)
-    col1, scores1, _ = ops.block_score_topk(prep, pol, row_ptr1, want_scores=True)
-    qp = orc.apply_permutation(q[:, :1].float().cpu(), full)
-    kp = orc.apply_permutation(k[:, :1].float().cpu(), full)
+    sh = [0, H - 1]
+    prep = ops.prepare_qkv(q[:, sh].contiguous(), k[:, sh].contiguous(), v[:, sh].contiguous(), perm_d, lay)
+    row_ptr2 = torch.from_numpy(pol.row_ptr(len(sh))).to(dev)
+    _, scores2, _ = ops.block_score_topk(prep, pol, row_ptr2, want_scores=True)
+    qp = orc.apply_permutation(q[:, sh].float().cpu(), full)
+    kp = orc.apply_permutation(k[:, sh].float().cpu(), full)
     ref_scores = orc.block_scores(qp, kp, cfg.tile, 128, cfg.video_len if hy else None, head_chunk=1)
-    torch.testing.assert_close(scores1.cpu(), ref_scores, rtol=2e-3, atol=1e-6)
-    got = scores1.cpu()
+    got = scores2.cpu()
+    err_t = (got.double() - ref_scores.double()).abs()
+    print(f"cfg{cfg_id} scores, heads {sh}: max abs error {float(err_t.max()):.2e}, max relative error "
+          f"{float((err_t / ref_scores.double().abs().clamp_min(1e-30)).max()):.2e}", flush=True)
+    torch.testing.assert_close(got, ref_scores, rtol=1e-4, atol=1e-9)
     sel = (orc.mask_from_scores_hunyuan(got, cfg.sparsity, L, cfg.video_len) if hy
            else orc.mask_from_scores_wan(got, cfg.sparsity))
-    assert torch.equal(mask[:1], sel)
+    assert torch.equal(mask[sh], sel)
     # selection from the oracle's own fp32 scores: a row may differ only where
     # its k-th and (k+1)-th oracle scores lie closer than twice the measured
     # score error (two scores each off by at most that much can swap)
     ref_sel = (orc.mask_from_scores_hunyuan(ref_scores, cfg.sparsity, L, cfg.video_len) if hy
                else orc.mask_from_scores_wan(ref_scores, cfg.sparsity))
-    err = float((got - ref_scores).abs().max())
+    err = float(err_t.max())
     n_cand = cfg.video_len // 128 if hy else kb
     kpick = topk_count(cfg.sparsity, kb) - (kb - n_cand if hy else 0)
     rows = ref_scores.shape[1]
-    differ = [r for r in range(rows) if not torch.equal(ref_sel[0, r], mask[0, r])]
+    differ = [(i, r) for i in range(len(sh)) for r in range(rows) if not torch.equal(ref_sel[i, r], mask[sh[i], r])]
     gaps = []
-    for r in differ:
-        top = torch.sort(ref_scores[0, r, :n_cand], descending=True).values
+    for i, r in differ:
+        top = torch.sort(ref_scores[i, r, :n_cand], descending=True).values
         gaps.append(float(top[kpick - 1] - top[kpick]))
-    print(f"cfg{cfg_id} head 0: {len(differ)} of {rows} rows select differently from the oracle's fp32 scores; "
-          f"max score error {err:.2e}, largest k-th/(k+1)-th gap among them "
-          f"{max(gaps) if gaps else 0.0:.2e}", flush=True)
+    print(f"cfg{cfg_id} heads {sh}: {len(differ)} of {len(sh) * rows} rows select differently from the oracle's "
+          f"fp32 scores; largest k-th/(k+1)-th gap among them {max(gaps) if gaps else 0.0:.2e}", flush=True)
     assert all(g <= 2 * err for g in gaps), (gaps, err)
-    assert len(differ) <= rows // 50
+    assert len(differ) <= len(sh) * rows // 50
 
-    # sampled query blocks of heads 0 and H-1 against fp32 masked attention
-    heads = [0, H - 1]
-    qbs = [0, 1, lay.q_blocks // 2, lay.q_blocks - 2, lay.q_blocks - 1]
+    # sampled query blocks of four heads against fp32 masked attention: eight
+    # blocks spread over the rows, the last three included (HunyuanVideo's
+    # dense text rows at configs[2])
+    heads = [0, H // 3, (2 * H) // 3, H - 1]
+    nq = lay.q_blocks
+    qbs = sorted({0, 1, nq // 4, nq // 2, (3 * nq) // 4, nq - 3, nq - 2, nq - 1})
     sub = [orc.apply_permutation(t[:, heads].float().cpu(), full) for t in (q, k, v)]
     ref = orc.masked_attention(*sub, mask[heads], 128, q_blocks=qbs)
     got_out = out[:, heads].cpu()[:, :, full]  # execution order
@@ -105,8 +113,10 @@ def test_full_size_call(dev, cfg_id):
     out32 = ops.bsa_fwd(prep_all, entry["row_ptr"], entry["col_idx"], out_dtype=torch.float32)
     g32 = out32[:, heads].cpu()[:, :, rows]
     max_abs, mr = float((g32 - r).abs().max()), _rel(g32, r)
-    print(f"cfg{cfg_id} fp32 output, sampled blocks: max-abs {max_abs:.2e}, mean-rel {mr:.2e}", flush=True)
-    assert max_abs <= 2e-2 and mr <= 1e-3
+    print(f"cfg{cfg_id} fp32 output, {len(heads)} heads x {len(qbs)} blocks: max-abs {max_abs:.2e}, "
+          f"mean-rel {mr:.2e}", flush=True)
+    # contract: max-abs 2e-2, mean-rel 1e-3; held here to 5e-4 (measured ~2.4e-4)
+    assert max_abs <= 2e-2 and mr <= 5e-4
     DFS_Attention.clear_cache()
     _dfs_attention_instances.clear()
 

@@ -65,6 +65,21 @@ def test_full_attention_flash_segments_and_cross(dev):
     assert _rel(out, _sdpa32(q, kc, vc)) < 4e-3
 
 
+def test_full_attention_flash_many_host_segments(dev):
+    """Host cu_seqlens of more than two segments (beyond the device varlen
+    path) run segment by segment, each square segment on the native kernel."""
+    from dfsattn_amd.fullattention import full_attention
+    g = torch.Generator().manual_seed(6)
+    L = 700
+    bounds = [0, 200, 201, 530, L]
+    q, k, v = (torch.randn(1, 2, L, 128, generator=g).to(torch.bfloat16) for _ in range(3))
+    cu = torch.tensor(bounds, dtype=torch.int32)
+    out = full_attention(q.to(dev), k.to(dev), v.to(dev), mode="flash", cu_seqlens_q=cu, cu_seqlens_kv=cu,
+                         max_seqlen_q=L, max_seqlen_kv=L).cpu()
+    ref = torch.cat([_sdpa32(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b]) for a, b in zip(bounds, bounds[1:])], dim=2)
+    assert _rel(out, ref) < 4e-3 and float((out.float() - ref).abs().max()) < 2e-2
+
+
 def _stub(dim, heads, dev, norm_shape=None, added_q=False):
     from stubs import StubAttention
     torch.manual_seed(3)

@@ -34,11 +34,21 @@ def test_hilbert_c_matches_numpy_oracle(grid):
 def test_abi_rejects_bad_arguments_without_launching():
     fake = ctypes.c_void_p(16)
     with pytest.raises(_lib.DfsKernelError, match="head_dim=96"):
-        _lib.call("dfs_prepare_qkv", fake, fake, fake, fake, 2, 1000, 96, 0, 1000, 16, 1,
+        _lib.call("dfs_prepare_qkv", fake, fake, fake, fake, 2, 1000, 96, 0, 1000, 16, 16, 1,
                   fake, fake, fake, None, None, None, None, None, None)
-    with pytest.raises(_lib.DfsKernelError, match="tile_size"):
-        _lib.call("dfs_prepare_qkv", fake, fake, fake, fake, 2, 1000, 128, 0, 1000, 24, 1,
+    with pytest.raises(_lib.DfsKernelError, match="q_tile_size=24"):
+        _lib.call("dfs_prepare_qkv", fake, fake, fake, fake, 2, 1000, 128, 0, 1000, 24, 16, 1,
                   fake, fake, fake, None, None, None, None, None, None)
+    with pytest.raises(_lib.DfsKernelError, match="k_tile_size=48"):
+        _lib.call("dfs_prepare_qkv", fake, fake, fake, fake, 2, 1000, 128, 0, 1000, 16, 48, 1,
+                  fake, fake, fake, None, None, None, None, None, None)
+    # scoring: tiles below 4 tokens, and the generic scorer without scores_out
+    with pytest.raises(_lib.DfsKernelError, match="k_tile_size=2"):
+        _lib.call("dfs_block_score_topk", fake, fake, fake, fake, 2, 128, 16, 2, 8, 8, 8, 8, 2, 8, 8,
+                  fake, fake, None, None, None, 0, None)
+    with pytest.raises(_lib.DfsKernelError, match="pass one"):
+        _lib.call("dfs_block_score_topk", fake, fake, fake, fake, 2, 128, 8, 64, 8, 8, 8, 8, 2, 8, 8,
+                  fake, fake, None, None, None, 0, None)
     with pytest.raises(_lib.DfsKernelError, match="k_pick"):
         _lib.call("dfs_topk_from_scores", fake, 2, 8, 8, 8, 8, 9, 8, 8, fake, fake, None, None)
     with pytest.raises(_lib.DfsKernelError, match="f16 inputs"):
@@ -58,7 +68,7 @@ def test_abi_rejects_bad_arguments_without_launching():
     # the allocation-free scorer refuses block sums beyond its 96 MiB scratch
     # before touching a device (64 heads x 1000 x 1000 blocks = 256 MB)
     with pytest.raises(_lib.DfsKernelError, match="scratch holds 100663296"):
-        _lib.call("dfs_block_score_topk_noalloc", fake, fake, fake, fake, 64, 128, 16, 1000, 1000, 1000, 1000, 300,
+        _lib.call("dfs_block_score_topk_noalloc", fake, fake, fake, fake, 64, 128, 16, 16, 1000, 1000, 1000, 1000, 300,
                   1000, 1000, fake, fake, None, None)
     with pytest.raises(_lib.DfsKernelError, match="row_bytes"):
         _lib.call("dfs_permute_gather", fake, fake, fake, 1, 10, 10, 10, 3, None)
@@ -171,3 +181,54 @@ def test_morton_bit_spreading_and_dispatch():
     assert torch.equal(od.video_perm_for("blk", 3, 8, 8), od.block3d_perm(3, 8, 8, 4, 4, 4))
     with pytest.raises(ValueError):
         od.video_perm_for("zigzag", 1, 2, 2)
+
+
+def test_workspace_size_by_tile_pair():
+    """The one-pass workspace exists for equal 16- or 32-token tiles only;
+    other valid pairs report 0 (two-pass generic scorer), invalid ones -1."""
+    ws = _lib.lib().dfs_block_score_topk_workspace_size
+    assert ws(40, 16, 16, 591, 591) > 0 and ws(40, 32, 32, 591, 591) > 0
+    for qt, kt in ((8, 64), (16, 32), (128, 4), (64, 64), (8, 8)):
+        assert ws(40, qt, kt, 591, 591) == 0
+    for qt, kt in ((2, 16), (16, 24), (256, 16), (0, 16)):
+        assert ws(40, qt, kt, 591, 591) == -1
+
+
+def test_noalloc_wrapper_runs_under_the_tensors_device(monkeypatch):
+    """ops.block_score_topk_noalloc makes the tensors' device current around
+    the C call (the library takes its scratch from the stream's device, and
+    the launch and the stream then agree whichever device the caller has
+    current). Host logic only: the device context and the C call are
+    recorded, nothing runs on a GPU."""
+    from types import SimpleNamespace
+    from dfsattn_amd.layout import ScoringLayout, wan_policy
+
+    events = []
+
+    class FakeDeviceCtx:
+        def __init__(self, dev):
+            self.dev = dev
+
+        def __enter__(self):
+            events.append(("enter", self.dev))
+
+        def __exit__(self, *exc):
+            events.append(("exit", self.dev))
+
+    target = torch.device("cuda", 3)
+    fake_t = SimpleNamespace(device=target)
+    layout = ScoringLayout(1024, 1024, 16)
+    pol = wan_policy(layout, 0.3)
+    prep = SimpleNamespace(q_hi=fake_t, q_lo=fake_t, k_hi=fake_t, k_lo=fake_t, q_perm=fake_t, heads=2,
+                           head_dim=64, layout=layout)
+    real_empty = torch.empty
+    monkeypatch.setattr(ops, "_require_device", lambda *a: None)
+    monkeypatch.setattr(ops, "_require_int32", lambda **k: None)
+    monkeypatch.setattr(ops, "_ptr", lambda t: None)
+    monkeypatch.setattr(ops, "_stream", lambda t: None)
+    monkeypatch.setattr(ops.torch, "empty", lambda *a, device=None, **k: real_empty(*a, **k))
+    monkeypatch.setattr(ops.torch.cuda, "device", FakeDeviceCtx)
+    monkeypatch.setattr(ops._lib, "call", lambda name, *args: events.append(("call", name, args[6], args[7])))
+    row_ptr = torch.from_numpy(pol.row_ptr(2))
+    ops.block_score_topk_noalloc(prep, pol, row_ptr)
+    assert events == [("enter", target), ("call", "dfs_block_score_topk_noalloc", 16, 16), ("exit", target)]

@@ -100,8 +100,10 @@ def test_hilbert3d_perm_is_a_permutation_with_local_steps(grid):
 
 
 # ---- a5/a6: scoring, brute force on a tiny input
-def _brute_block_scores(qp, kp, tile, block, video_len):
-    """Loop restatement of attention_wan.py:176-246 / attention_hyvideo.py:331-422."""
+def _brute_block_scores(qp, kp, tile, block, video_len, k_tile=None):
+    """Loop restatement of attention_wan.py:176-246 / attention_hyvideo.py:331-422
+    (query tiles of ``tile`` tokens, key tiles of ``k_tile``)."""
+    k_tile = tile if k_tile is None else k_tile
     _, heads, seq_len, dim = qp.shape
     vb, kb = math.ceil(video_len / block), math.ceil(seq_len / block)
     layout = [None] * (kb * block)
@@ -111,31 +113,41 @@ def _brute_block_scores(qp, kp, tile, block, video_len):
         layout[vb * block + t] = video_len + t
     out = torch.zeros(heads, vb, kb, dtype=torch.float64)
     for h in range(heads):
-        def tile_mean(x, t):
+        def tile_mean(x, t, size):
             acc = torch.zeros(dim, dtype=torch.float64)
-            for p in range(t * tile, (t + 1) * tile):
+            for p in range(t * size, (t + 1) * size):
                 if layout[p] is not None:
                     acc += x[0, h, layout[p]].double()
-            return acc / tile
-        qt = [tile_mean(qp, t) for t in range(vb * block // tile)]
-        kt = [tile_mean(kp, t) for t in range(kb * block // tile)]
+            return acc / size
+        qt = [tile_mean(qp, t, tile) for t in range(vb * block // tile)]
+        kt = [tile_mean(kp, t, k_tile) for t in range(kb * block // k_tile)]
         for i, qi in enumerate(qt):
             s = torch.stack([qi @ kj for kj in kt]) / math.sqrt(dim)
             p = torch.exp(s - s.max())
             p = p / p.sum()
             for j in range(len(kt)):
-                out[h, i // (block // tile), j // (block // tile)] += p[j]
+                out[h, i // (block // tile), j // (block // k_tile)] += p[j]
     return out
 
 
-@pytest.mark.parametrize("seq,video,tile", [(300, 300, 16), (256, 256, 32), (290, 250, 16)])
-def test_block_scores_match_brute_force(seq, video, tile):
+@pytest.mark.parametrize("seq,video,tile,k_tile", [
+    (300, 300, 16, 16), (256, 256, 32, 32), (290, 250, 16, 16),
+    (300, 300, 8, 64), (290, 250, 128, 4), (300, 200, 64, 32)])
+def test_block_scores_match_brute_force(seq, video, tile, k_tile):
     torch.manual_seed(0)
     qp, kp = torch.randn(1, 2, seq, 8), torch.randn(1, 2, seq, 8)
-    got = orc.block_scores(qp, kp, tile, 128, None if seq == video else video)
-    ref = _brute_block_scores(qp, kp, tile, 128, video)
+    got = orc.block_scores(qp, kp, tile, 128, None if seq == video else video, k_tile=k_tile)
+    ref = _brute_block_scores(qp, kp, tile, 128, video, k_tile)
     assert torch.allclose(got.double(), ref, rtol=1e-5, atol=1e-7)
     assert torch.allclose(got.sum(-1).double(), torch.full_like(ref.sum(-1), 128 / tile), rtol=1e-5)
+
+
+def test_block_scores_reject_tiles_not_dividing_the_block():
+    qp = torch.randn(1, 1, 256, 8)
+    with pytest.raises(AssertionError, match="k_tile_size"):
+        orc.block_scores(qp, qp, 16, 128, k_tile=48)
+    with pytest.raises(AssertionError, match="q_tile_size"):
+        orc.block_scores(qp, qp, 24, 128)
 
 
 def test_wan_mask_matches_torch_topk_on_tie_free_scores():
