@@ -20,6 +20,10 @@ a less local mask at the same density (K drawn from a field of its own, so a
 row's kept blocks spread over the whole row): its whole-call median and its
 attention kernel time.
 
+The default line also carries the second BASELINE configuration under
+``cfg2``: the HunyuanVideo call's time, phases and attention-kernel fraction
+of peak over 10 fresh-mask calls (skipped with ``--headline-only``).
+
 ``--workload cfg2`` measures the HunyuanVideo call instead (configs[2]:
 118,800 video + 256 text tokens, 24 heads), and ``--workload cfg3`` the
 mask-cache regime (configs[3]: 50 denoising calls at the cfg1 shape with
@@ -604,6 +608,19 @@ def main():
         return
     res = run_gpu(args)
     inputs = res.pop("inputs")
+    cfg2 = None
+    if not args.headline_only:
+        # The second BASELINE configuration (HunyuanVideo joint attention,
+        # configs[2]) as extra keys of the same line: whole call, phases and
+        # the attention kernel's fraction of peak over a few fresh-mask calls.
+        log("cfg2 (HunyuanVideo shape) for the extra keys")
+        c2 = run_cfg2(argparse.Namespace(steps=10, warmup=3, text_valid=None))
+        torch.cuda.empty_cache()
+        cfg2 = {"workload": "configs[2]: 33x45x80 video + 256 text tokens (119,056), 24 heads, d128, bf16, tile 16, "
+                            "sparsity 0.3, fresh mask per call; 10 timed calls after 3 untimed",
+                "call_ms": c2["value"], "attention_ms": c2["phases_ms"]["attention"],
+                "attention_tflops": c2["attention_kernel"]["tflops"], "attention_frac": c2["attention_kernel"]["frac"],
+                "call_frac": c2["frac_of_bf16_peak"], "phases_ms": c2["phases_ms"], "kept_flop": c2["kept_flop"]}
     cpu = None if args.no_cpu_baseline else cpu_baseline(*inputs)
     del inputs
     att_ms = res["phase_ms"]["attention"]
@@ -635,6 +652,7 @@ def main():
         "prepare_gbs": round(res["prepare_gbs"], 1),
         "kept_density": round(res["density"], 4),
         **res["side"],
+        "cfg2": cfg2,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
