@@ -32,7 +32,8 @@ SIGNATURES = {
                                      _i64, _i64, _i64, _p, _p, _p, _p],
     "dfs_topk_from_scores": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p],
     "dfs_prepare_fixup": [_p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p],
-    "dfs_bsa_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _p, _i32, _p, _p, _p, _p, _i64, _p, _p],
+    "dfs_bsa_fwd": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _p, _i32, _p, _p, _p, _p, _i64, _p,
+                    _p, _p, _i32, _p],
     "dfs_mask_row_counts": [_p, _i64, _i64, _p, _p],
     "dfs_mask_to_csr": [_p, _i64, _i64, _p, _p, _p],
     "dfs_csr_to_mask": [_p, _p, _i64, _i64, _p, _p],
@@ -44,7 +45,7 @@ SIGNATURES = {
     "dfs_gated_residual": [_p, _p, _p, _i64, _i64, _i32, _p, _p],
 }
 _RESTYPES = {"dfs_last_error": ctypes.c_char_p, "dfs_block_score_topk_workspace_size": ctypes.c_int64}
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib = None

@@ -77,8 +77,9 @@ class DfsCore:
     _entry_fields: Tuple[str, ...] = ("block_mask", "block_indices", "flex_block_mask")
 
     def _prepare(self, q, k, v, perm, layout, pool: bool) -> "ops.Prepared":
+        # No permuted Q: the attention kernel gathers Q rows from the input.
         return ops.prepare_qkv(q, k, v, perm, layout, operand_dtype=operand_dtype_for(q.dtype, self.operand_dtype),
-                               pool=pool)
+                               pool=pool, q_operand=False)
 
     # --- permutation -----------------------------------------------------
     def _device_permutation(self, seq_len: int, device: torch.device) -> torch.Tensor:
@@ -161,7 +162,7 @@ class DfsCore:
     def _select(self, prep: ops.Prepared, layout: ScoringLayout, sparse_ratio: float,
                 want_scores: bool = False) -> MaskEntry:
         policy = self._policy(layout, sparse_ratio)
-        row_ptr = row_ptr_for(policy, prep.heads, prep.q_perm.device)
+        row_ptr = row_ptr_for(policy, prep.heads, prep.device)
         col_idx, scores, _ = ops.block_score_topk(prep, policy, row_ptr, want_scores=want_scores)
         entry = MaskEntry(row_ptr=row_ptr, col_idx=col_idx, policy=policy, heads=prep.heads,
                           **{field: None for field in self._entry_fields})

@@ -61,7 +61,29 @@ struct BsaParams {
   const int32_t* cu_q;
   const int32_t* cu_k;
   const int32_t* exps;
+  // Optional Q source read in place of q_perm: execution row r < L is input
+  // row q_rows[r] of q_src ([H][L][D], f16 when q_src_f16, else bf16), rows
+  // past L are zero. Its exponent exps[0][h] is then only a range mark: the
+  // values are read unscaled.
+  const uint16_t* q_src;
+  const int32_t* q_rows;
+  int q_src_f16;
 };
+
+// Start of the D-element Q row of execution row qrow of head h: q_perm's row,
+// or the input row it comes from (nullptr for a zero row past L). f16 tells
+// whether the row holds f16 (else bf16) values.
+template <int D>
+__device__ __forceinline__ const uint16_t* q_row_ptr(const uint16_t* __restrict__ q, const BsaParams& p, int h,
+                                                     int qrow, bool& f16) {
+  if (p.q_src) {
+    f16 = p.q_src_f16 != 0;
+    if (qrow >= p.L) return nullptr;
+    return p.q_src + (static_cast<int64_t>(h) * p.L + p.q_rows[qrow]) * D;
+  }
+  f16 = true;
+  return q + (static_cast<int64_t>(h) * p.R + qrow) * D;
+}
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -130,9 +152,11 @@ __device__ __forceinline__ bool wg_coords(const BsaParams& p, int& h, int& qb) {
 template <int D, typename QkOp>
 __device__ __forceinline__ void load_q(const uint16_t* __restrict__ q, const BsaParams& p, int h, int qrow,
                                        int hl, typename QkOp::vec* qf) {
-  const uint4* src = reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(h) * p.R + qrow) * D);
+  bool f16;  // the bf16-operand path takes bf16 rows only (q_perm or a bf16 q_src)
+  const uint4* src = reinterpret_cast<const uint4*>(q_row_ptr<D>(q, p, h, qrow, f16));
 #pragma unroll
-  for (int s = 0; s < D / 16; ++s) qf[s] = __builtin_bit_cast(typename QkOp::vec, src[2 * s + hl]);
+  for (int s = 0; s < D / 16; ++s)
+    qf[s] = __builtin_bit_cast(typename QkOp::vec, src ? src[2 * s + hl] : make_uint4(0, 0, 0, 0));
 }
 
 // S^T (128 keys x this wave's 32 queries) = K Q^T from an LDS K tile; the
@@ -225,21 +249,24 @@ __device__ __forceinline__ void pv_tile(const uint16_t* v_tile, const f32x16* s,
 // would leave the f16 range is stored as q c' 2^-r (r > 0, the smallest
 // power of two that fits): its S arrives as S 2^-r and the kernel multiplies
 // it by row_scale = 2^r. The common instance runs heads without exponents at
-// a scale where |q_perm c| < 2^15 always holds.
+// a scale where |q c| < 2^15 always holds (f16 q_perm values, or Q source
+// values of a head inside the f16 range, times c < 0.5).
 template <int D, bool SCALED>
 __device__ __forceinline__ void load_q_scaled(const uint16_t* __restrict__ q, const BsaParams& p, int h, int qrow,
                                               int hl, f16x8* qf, float& row_scale) {
   float c = p.scale_log2;
-  if (SCALED && p.exps) c = ldexpf(c, p.exps[h] + p.exps[p.H + h]);
-  const uint4* src = reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(h) * p.R + qrow) * D);
+  // q_perm holds q 2^-eq; a Q source is read unscaled
+  if (SCALED && p.exps) c = ldexpf(c, (p.q_src ? 0 : p.exps[h]) + p.exps[p.H + h]);
+  bool f16;
+  const uint4* src = reinterpret_cast<const uint4*>(q_row_ptr<D>(q, p, h, qrow, f16));
   float x[D / 16][8];
   float mx = 0.f;
 #pragma unroll
   for (int s = 0; s < D / 16; ++s) {
-    const f16x8 v = __builtin_bit_cast(f16x8, src[2 * s + hl]);
+    const uint4 raw = src ? src[2 * s + hl] : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      x[s][i] = static_cast<float>(v[i]) * c;
+      x[s][i] = (f16 ? f16_bits_to_f32(u16_at(raw, i)) : bf16_bits_to_f32(u16_at(raw, i))) * c;
       if (SCALED) mx = fmaxf(mx, fabsf(x[s][i]));
     }
   }
@@ -674,6 +701,9 @@ struct SegParams {
   const int32_t* cu_k;
   int n_seq;
   const int32_t* exps;  // optional [3][H]
+  const uint16_t* q_src;  // optional Q source (as in BsaParams)
+  const int32_t* q_rows;
+  int q_src_f16;
 };
 
 __device__ __forceinline__ float operand_at(const uint16_t* base, int64_t i, bool f16) {
@@ -719,7 +749,7 @@ __global__ void __launch_bounds__(256) bsa_segment_kernel(const uint16_t* __rest
   const bool qk16 = p.qk_f16 != 0, pv16 = p.pv_f16 != 0;
   float sq = p.scale_log2, sv = 1.f;
   if (p.exps) {
-    sq = ldexpf(sq, p.exps[h] + p.exps[p.H + h]);
+    sq = ldexpf(sq, (p.q_src ? 0 : p.exps[h]) + p.exps[p.H + h]);  // a Q source is read unscaled
     sv = ldexpf(1.f, p.exps[2 * p.H + h]);
   }
   auto wave_sync = [] {
@@ -729,6 +759,13 @@ __global__ void __launch_bounds__(256) bsa_segment_kernel(const uint16_t* __rest
   auto half_to_f32 = [](uint32_t bits, bool f16) { return f16 ? f16_bits_to_f32(bits) : bf16_bits_to_f32(bits); };
   const int64_t hq = static_cast<int64_t>(h) * p.R * D;
   const uint4* krows = reinterpret_cast<const uint4*>(k + hq);
+  // Element j of execution row r's query (r < L).
+  auto q_at = [&](int r, int j) -> float {
+    if (p.q_src)
+      return operand_at(p.q_src, (static_cast<int64_t>(h) * p.L + p.q_rows[r]) * D + j, p.q_src_f16 != 0);
+    return operand_at(q, hq + static_cast<int64_t>(r) * D + j, qk16);
+  };
+
   for (int r0 = cq1 + RG * wave; r0 < p.L; r0 += RG * n_waves) {
     float o[RG][DPL], m[RG], l[RG];
 #pragma unroll
@@ -742,7 +779,7 @@ __global__ void __launch_bounds__(256) bsa_segment_kernel(const uint16_t* __rest
 #pragma unroll
       for (int i = 0; i < RG; ++i)
         for (int j = lane; j < D; j += 64)
-          qs[w][i][j] = r0 + i < cq2 ? operand_at(q, hq + static_cast<int64_t>(r0 + i) * D + j, qk16) * sq : 0.f;
+          qs[w][i][j] = r0 + i < cq2 ? q_at(r0 + i, j) * sq : 0.f;
       wave_sync();
       const int64_t crow = static_cast<int64_t>(h) * p.csr_qb + ((r0 - cq1) >> 7);
       const int beg = row_ptr[crow], end = row_ptr[crow + 1];
@@ -895,10 +932,16 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
                            int64_t seq_len, int64_t head_dim, int dtype, int pv_dtype, float scale,
                            void* out, int out_dtype, const int32_t* out_perm, float* lse,
                            const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t n_seq,
-                           const int32_t* exps, dfs_stream_t stream) {
+                           const int32_t* exps, const void* q_src, const int32_t* q_rows, int q_src_dtype,
+                           dfs_stream_t stream) {
   using namespace dfs;
   const char* name = "dfs_bsa_fwd";
-  DFS_REQUIRE(q_perm && k_perm && v_t && row_ptr && col_idx && out, "%s: NULL operand", name);
+  DFS_REQUIRE((q_perm || q_src) && k_perm && v_t && row_ptr && col_idx && out, "%s: NULL operand", name);
+  DFS_REQUIRE(!q_src || q_rows, "%s: q_src needs q_rows", name);
+  DFS_REQUIRE(!q_src || q_src_dtype == DFS_DTYPE_BF16 || q_src_dtype == DFS_DTYPE_F16,
+              "%s: q_src_dtype=%d (supported: bf16, f16)", name, q_src_dtype);
+  DFS_REQUIRE(!q_src || dtype == DFS_DTYPE_F16 || q_src_dtype == DFS_DTYPE_BF16,
+              "%s: bf16 Q/K operands need a bf16 q_src", name);
   DFS_REQUIRE(head_dim == 64 || head_dim == 128, "%s: head_dim=%lld (supported: 64, 128)", name,
               (long long)head_dim);
   DFS_REQUIRE(dtype == DFS_DTYPE_BF16 || dtype == DFS_DTYPE_F16, "%s: dtype=%d (supported: bf16, f16)",
@@ -937,6 +980,9 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
   p.cu_q = cu_seqlens_q;
   p.cu_k = cu_seqlens_k;
   p.exps = exps;
+  p.q_src = static_cast<const uint16_t*>(q_src);
+  p.q_rows = q_rows;
+  p.q_src_f16 = q_src_dtype == DFS_DTYPE_F16 ? 1 : 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool qk_f16 = dtype == DFS_DTYPE_F16, pv_f16 = pv_dtype == DFS_DTYPE_F16;
   if (head_dim == 128)
@@ -958,6 +1004,9 @@ extern "C" int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v
     sp.cu_k = cu_seqlens_k;
     sp.n_seq = static_cast<int>(n_seq);
     sp.exps = exps;
+    sp.q_src = p.q_src;
+    sp.q_rows = q_rows;
+    sp.q_src_f16 = p.q_src_f16;
     // Enough waves for a few hundred rows per head; each wave strides over
     // the rows after segment 0.
     const dim3 grid(16, static_cast<unsigned>(heads));

@@ -63,7 +63,7 @@ extern "C" {
 
 const char* dfs_last_error(void) { return dfs::g_error; }
 
-int dfs_abi_version(void) { return 4; }
+int dfs_abi_version(void) { return 5; }
 
 int dfs_hilbert3d_perm(int64_t f, int64_t h, int64_t w, int64_t* perm_out) {
   DFS_REQUIRE(f > 0 && h > 0 && w > 0, "hilbert3d_perm: grid %lldx%lldx%lld must be positive",

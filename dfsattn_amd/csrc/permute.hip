@@ -158,10 +158,13 @@ __device__ __forceinline__ void prep_qk_tiles(const PrepParams& p, int bx, int n
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const uint4* src = (is_k ? p.k : p.q) + static_cast<int64_t>(h) * p.L * CPR;
-  uint4* dst = (is_k ? p.k_perm : p.q_perm) + static_cast<int64_t>(h) * p.R * CPR;
+  // Without q_perm the attention kernel gathers its Q rows from the input
+  // itself: Q is then only pooled and range-flagged here.
+  const bool store = is_k || p.q_perm != nullptr;
+  uint4* dst = store ? (is_k ? p.k_perm : p.q_perm) + static_cast<int64_t>(h) * p.R * CPR : nullptr;
 
   // Zero-fill execution rows L..R-1 (done by the last block of each tensor/head).
-  if (bx == nbx - 1) {
+  if (store && bx == nbx - 1) {
     const int n = (p.R - p.L) * CPR;
     for (int i = threadIdx.x; i < n; i += blockDim.x)
       store_stream(dst + static_cast<int64_t>(p.L) * CPR + i, make_uint4(0, 0, 0, 0));
@@ -193,8 +196,8 @@ __device__ __forceinline__ void prep_qk_tiles(const PrepParams& p, int bx, int n
 #pragma unroll
     for (int b = 0; b < BATCH; ++b) {
       if (xs[b] < 0) continue;
-      store_stream(dst + static_cast<int64_t>(xs[b]) * CPR + c,
-                   p.convert ? bf16x8_to_f16x8(val[b], &overflow) : val[b]);
+      const uint4 op = p.convert ? bf16x8_to_f16x8(val[b], &overflow) : val[b];
+      if (store) store_stream(dst + static_cast<int64_t>(xs[b]) * CPR + c, op);
       add_chunk(acc, val[b], p.in_f16 != 0);  // tile means of the input values
     }
   }
@@ -354,7 +357,10 @@ __global__ void __launch_bounds__(1024) prep_fixup_kernel(PrepParams p, int32_t*
   for (int i = 0; i < static_cast<int>(blockDim.x >> 6); ++i) mx = fmaxf(mx, red[i]);
   const int e = mx >= 32768.f ? max(1, ilogbf(mx) - 14) : 1;
   const float sc = ldexpf(1.f, -e);
-  if (t < 2) {
+  if (t == 0 && p.q_perm == nullptr) {
+    // No Q operand to rewrite (the attention kernel reads Q from the input):
+    // e only marks the head as beyond the f16 range.
+  } else if (t < 2) {
     uint4* dst = (t == 0 ? p.q_perm : p.k_perm) + static_cast<int64_t>(h) * p.R * CPR;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
       const int x = i / CPR, c = i - x * CPR;
@@ -418,7 +424,7 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v, const int32_t* 
                     uint16_t* k_pool_hi, uint16_t* k_pool_lo, int32_t* overflow,
                     dfs_stream_t stream) {
   using namespace dfs;
-  DFS_REQUIRE(q && k && v && perm && q_perm && k_perm && v_t, "dfs_prepare_qkv: NULL operand");
+  DFS_REQUIRE(q && k && v && perm && k_perm && v_t, "dfs_prepare_qkv: NULL operand");
   DFS_REQUIRE(head_dim == 64 || head_dim == 128, "dfs_prepare_qkv: head_dim=%lld (supported: 64, 128)",
               (long long)head_dim);
   DFS_REQUIRE(dtype == DFS_DTYPE_BF16 || dtype == DFS_DTYPE_F16,
@@ -492,7 +498,7 @@ int dfs_prepare_fixup(const void* q, const void* k, const void* v, const int32_t
                       int64_t seq_len, int64_t head_dim, void* q_perm, void* k_perm, void* v_t,
                       int32_t* overflow, int32_t* exps, dfs_stream_t stream) {
   using namespace dfs;
-  DFS_REQUIRE(q && k && v && perm && q_perm && k_perm && v_t && overflow && exps, "dfs_prepare_fixup: NULL operand");
+  DFS_REQUIRE(q && k && v && perm && k_perm && v_t && overflow && exps, "dfs_prepare_fixup: NULL operand");
   DFS_REQUIRE(head_dim == 64 || head_dim == 128, "dfs_prepare_fixup: head_dim=%lld (supported: 64, 128)",
               (long long)head_dim);
   DFS_REQUIRE(heads > 0 && heads < 65536, "dfs_prepare_fixup: heads=%lld out of range", (long long)heads);

@@ -61,7 +61,8 @@ def dense_attention_native(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     kernel does, without a host read."""
     _, heads, length, _ = q.shape
     layout = ScoringLayout(length, length, 16)
-    prep = ops.prepare_qkv(q, k, v, _identity(q.device, length), layout, operand_dtype=operand_dtype, pool=False)
+    prep = ops.prepare_qkv(q, k, v, _identity(q.device, length), layout, operand_dtype=operand_dtype, pool=False,
+                           q_operand=False)
     row_ptr, col_idx = _dense_csr(q.device, heads, length)
     return ops.bsa_fwd(prep, row_ptr, col_idx, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k)
 

@@ -114,7 +114,7 @@ class Prepared:
     head_dim: int
     dtype: torch.dtype          # input dtype (and the default output dtype)
     operand_dtype: torch.dtype  # dtype of q_perm, k_perm and v_t
-    q_perm: torch.Tensor  # [H, R, D]
+    q_perm: Optional[torch.Tensor]  # [H, R, D]; None: the attention reads q_src through q_rows
     k_perm: torch.Tensor  # [H, R, D]
     v_t: torch.Tensor     # [H, R/128, D, 128]
     q_hi: Optional[torch.Tensor] = None  # [H, q_tiles, D] bf16
@@ -125,17 +125,29 @@ class Prepared:
     # and v_t hold x * 2^-e for heads whose bf16 inputs exceed the f16 range);
     # None when the operands keep the inputs' dtype.
     exps: Optional[torch.Tensor] = None
+    # Without q_perm: the contiguous input Q [H, L, D] and the int32
+    # permutation (execution row r reads input row q_rows[r]).
+    q_src: Optional[torch.Tensor] = None
+    q_rows: Optional[torch.Tensor] = None
+
+    @property
+    def device(self) -> torch.device:
+        return self.k_perm.device
 
 
 def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.Tensor,
-                layout: ScoringLayout, operand_dtype: Optional[torch.dtype] = None, pool: bool = True) -> Prepared:
+                layout: ScoringLayout, operand_dtype: Optional[torch.dtype] = None, pool: bool = True,
+                q_operand: bool = True) -> Prepared:
     """Gathers Q, K, V into execution order (V block-transposed) and, with
     ``pool``, writes the tile means used for scoring. ``operand_dtype`` (f16
     by default) is the dtype of the attention operands: f16 rounds bf16
     inputs to f16; bf16 keeps their bits. With f16 operands from bf16 inputs
     every finite input is kept: a head whose values exceed the f16 range is
     stored scaled by an exact power of two (``Prepared.exps``), decided and
-    applied on the device without a host round trip."""
+    applied on the device without a host round trip. Without ``q_operand``
+    no permuted Q is written: the attention kernel gathers each Q row from
+    the input itself (one read per row either way), which saves one write
+    of Q per call."""
     _require_device(q, k, v, perm)
     _require_int32(perm=perm)
     heads, length, dim = _heads_rows(q)
@@ -155,10 +167,12 @@ def prepare_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, perm: torch.T
     rows = layout.rows
     prep = Prepared(
         layout=layout, heads=heads, head_dim=dim, dtype=q.dtype, operand_dtype=operand_dtype,
-        q_perm=torch.empty((heads, rows, dim), dtype=operand_dtype, device=dev),
+        q_perm=torch.empty((heads, rows, dim), dtype=operand_dtype, device=dev) if q_operand else None,
         k_perm=torch.empty((heads, rows, dim), dtype=operand_dtype, device=dev),
         v_t=torch.empty((heads, rows // 128, dim, 128), dtype=operand_dtype, device=dev),
     )
+    if not q_operand:
+        prep.q_src, prep.q_rows = q, perm
     if pool:
         prep.q_hi = torch.empty((heads, layout.q_tiles, dim), dtype=torch.bfloat16, device=dev)
         prep.q_lo = torch.empty_like(prep.q_hi)
@@ -209,7 +223,7 @@ def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
     _require_int32(row_ptr=row_ptr)
     if row_ptr.numel() != prep.heads * policy.q_blocks + 1:
         raise ValueError(f"row_ptr has {row_ptr.numel()} entries for {prep.heads} x {policy.q_blocks} rows")
-    dev = prep.q_perm.device
+    dev = prep.device
     nnz = policy.nnz(prep.heads)
     col_idx = torch.empty(nnz, dtype=torch.int32, device=dev)
     q_tile, k_tile = prep.layout.q_tile, prep.layout.k_tile
@@ -224,7 +238,7 @@ def block_score_topk(prep: Prepared, policy: TopkPolicy, row_ptr: torch.Tensor,
     ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=dev) if one_pass_rows else None
     _lib.call("dfs_block_score_topk", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi), _ptr(prep.k_lo),
               prep.heads, prep.head_dim, q_tile, k_tile, *_policy_args(policy), _ptr(row_ptr),
-              _ptr(col_idx), _ptr(scores), _ptr(mask), _ptr(ws), ws_bytes, _stream(prep.q_perm))
+              _ptr(col_idx), _ptr(scores), _ptr(mask), _ptr(ws), ws_bytes, _stream(prep.k_perm))
     return col_idx, (scores if want_scores else None), mask
 
 
@@ -240,7 +254,7 @@ def block_score_topk_noalloc(prep: Prepared, policy: TopkPolicy, row_ptr: torch.
     _require_int32(row_ptr=row_ptr)
     if row_ptr.numel() != prep.heads * policy.q_blocks + 1:
         raise ValueError(f"row_ptr has {row_ptr.numel()} entries for {prep.heads} x {policy.q_blocks} rows")
-    dev = prep.q_perm.device
+    dev = prep.device
     col_idx = torch.empty(policy.nnz(prep.heads), dtype=torch.int32, device=dev)
     mask = (torch.empty((prep.heads, policy.q_blocks, policy.k_blocks), dtype=torch.uint8, device=dev)
             if want_mask else None)
@@ -250,7 +264,7 @@ def block_score_topk_noalloc(prep: Prepared, policy: TopkPolicy, row_ptr: torch.
     with torch.cuda.device(dev):
         _lib.call("dfs_block_score_topk_noalloc", _ptr(prep.q_hi), _ptr(prep.q_lo), _ptr(prep.k_hi),
                   _ptr(prep.k_lo), prep.heads, prep.head_dim, prep.layout.q_tile, prep.layout.k_tile,
-                  *_policy_args(policy), _ptr(row_ptr), _ptr(col_idx), _ptr(mask), _stream(prep.q_perm))
+                  *_policy_args(policy), _ptr(row_ptr), _ptr(col_idx), _ptr(mask), _stream(prep.k_perm))
     return col_idx, mask
 
 
@@ -297,7 +311,7 @@ def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale:
     kernel does: sequence i's queries [cq[i], cq[i+1]) attend its keys
     [ck[i], ck[i+1]) under the mask indexed from each sequence's start; rows
     in no query sequence are zero. The offsets stay on the device."""
-    _require_device(prep.q_perm, row_ptr, col_idx, out_perm, out, cu_seqlens_q, cu_seqlens_k)
+    _require_device(prep.k_perm, prep.q_perm, prep.q_src, row_ptr, col_idx, out_perm, out, cu_seqlens_q, cu_seqlens_k)
     _require_int32(row_ptr=row_ptr, col_idx=col_idx, out_perm=out_perm)
     if row_ptr.numel() != prep.heads * prep.layout.q_blocks + 1:
         raise ValueError(f"row_ptr has {row_ptr.numel()} entries for {prep.heads} x {prep.layout.q_blocks} rows")
@@ -305,13 +319,13 @@ def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale:
         raise ValueError("pass both cu_seqlens_q and cu_seqlens_k or neither")
     n_seq = 1
     if cu_seqlens_q is not None:
-        n_seq = _check_cu(cu_seqlens_q, "cu_seqlens_q", prep.q_perm.device)
-        if _check_cu(cu_seqlens_k, "cu_seqlens_k", prep.q_perm.device) != n_seq:
+        n_seq = _check_cu(cu_seqlens_q, "cu_seqlens_q", prep.device)
+        if _check_cu(cu_seqlens_k, "cu_seqlens_k", prep.device) != n_seq:
             raise ValueError("cu_seqlens_q and cu_seqlens_k describe different sequence counts")
     L = prep.layout.seq_len
     out_dtype = out_dtype or prep.dtype
     if out is None:
-        out = torch.empty((1, prep.heads, L, prep.head_dim), dtype=out_dtype, device=prep.q_perm.device)
+        out = torch.empty((1, prep.heads, L, prep.head_dim), dtype=out_dtype, device=prep.device)
     elif out.dtype != out_dtype or not out.is_contiguous() or out.numel() != prep.heads * L * prep.head_dim:
         raise ValueError("out must be a contiguous [1, H, L, D] tensor of out_dtype")
     lse = torch.empty((prep.heads, L), dtype=torch.float32, device=out.device) if want_lse else None
@@ -319,7 +333,8 @@ def bsa_fwd(prep: Prepared, row_ptr: torch.Tensor, col_idx: torch.Tensor, scale:
     _lib.call("dfs_bsa_fwd", _ptr(prep.q_perm), _ptr(prep.k_perm), _ptr(prep.v_t), _ptr(row_ptr),
               _ptr(col_idx), prep.heads, L, prep.head_dim, DTYPE_CODE[prep.operand_dtype],
               DTYPE_CODE[prep.operand_dtype], scale, _ptr(out), DTYPE_CODE[out_dtype], _ptr(out_perm),
-              _ptr(lse), _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), n_seq, _ptr(prep.exps), _stream(prep.q_perm))
+              _ptr(lse), _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), n_seq, _ptr(prep.exps), _ptr(prep.q_src),
+              _ptr(prep.q_rows), DTYPE_CODE[prep.dtype], _stream(prep.k_perm))
     return (out, lse) if want_lse else out
 
 

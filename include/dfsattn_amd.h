@@ -41,7 +41,8 @@ const char* dfs_last_error(void);
 
 /* ABI version; bumped whenever a signature below changes (2: scoring workspace; 3: device cu_seqlens
  * and per-head operand exponents in the attention call, per-head overflow flags and dfs_prepare_fixup;
- * 4: separate query and key tile sizes in preparation and scoring). */
+ * 4: separate query and key tile sizes in preparation and scoring; 5: Q read from the input by
+ * the attention kernel, q_perm optional). */
 int dfs_abi_version(void);
 
 /*
@@ -92,6 +93,8 @@ int dfs_permute_scatter(const void* src, const int32_t* perm, void* dst,
  *   k_pool_*     [H][ceil(L/128)*128/k_tile_size][D]  NULL to skip pooling:
  *                cached steps).
  *                Means of the input values, whatever operand_dtype.
+ *   q_perm       may be NULL: Q is then only pooled and range-flagged, and
+ *                dfs_bsa_fwd reads it from the input (q_src, q_rows).
  *   overflow     optional int32 [3][H] flags (Q, K, V per head), zeroed by
  *                the caller; entry [t][h] is set when bf16 inputs are
  *                rounded to f16 and a finite value of tensor t, head h
@@ -114,7 +117,8 @@ int dfs_prepare_qkv(const void* q, const void* k, const void* v,
  * that head's q_perm, k_perm or v_t from the inputs as x * 2^-e (e >= 1, the
  * smallest exponent that brings the head's largest finite |x| below 2^15)
  * and sets exps[t][h] = e; every other entry of exps ([3][H] int32) is set
- * to 0, and the flags are cleared. dfs_bsa_fwd takes exps and undoes the
+ * to 0, and the flags are cleared (with q_perm NULL a flagged Q head is only
+ * recorded in exps, nothing is rewritten). dfs_bsa_fwd takes exps and undoes the
  * factors exactly (powers of two). Heads within the f16 range cost one flag
  * read. No reference counterpart: the reference's kernel computes in bf16
  * (block_sparse_attn_func, attention_wan.py:379-386), whose range this keeps.
@@ -219,7 +223,8 @@ int dfs_topk_from_scores(const float* scores, int64_t heads,
 
 /*
  * Block-sparse flash-attention forward over the kept 128x128 blocks.
- *   q_perm, k_perm, v_t  as produced by dfs_prepare_qkv; dtype is the dtype
+ *   q_perm, k_perm, v_t  as produced by dfs_prepare_qkv (q_perm may be NULL
+ *                        with q_src below); dtype is the dtype
  *                        of q_perm and k_perm, pv_dtype that of v_t (f16/f16
  *                        and bf16/bf16 as prepared; bf16/f16 also accepted).
  *                        With f16 q_perm the kernel folds scale * log2(e)
@@ -247,6 +252,16 @@ int dfs_topk_from_scores(const float* scores, int64_t heads,
  *   exps                 optional int32 [3][H] per-head exponents written by
  *                        dfs_prepare_fixup (q_perm, k_perm, v_t hold
  *                        x * 2^-e); NULL means all zero.
+ *   q_src, q_rows        optional: Q read from the input instead of q_perm
+ *                        (which may then be NULL): execution row r < L is
+ *                        row q_rows[r] of q_src [H][L][D] (the permutation
+ *                        dfs_prepare_qkv took), in q_src_dtype (bf16 or f16;
+ *                        bf16 Q/K operands need bf16). Each workgroup reads
+ *                        its 128 rows once, so the gather costs nothing
+ *                        measurable and the preparation skips the q_perm
+ *                        write. exps[0][h] then only marks a head whose Q
+ *                        exceeds the f16 range (its rows are scaled by the
+ *                        kernel, row by row).
  * Keys past a sequence's end in its last block are masked out; rows with no
  * kept block give 0. CSR columns must ascend.
  * Replaces block_sparse_attn_func (attention_wan.py:379-386;
@@ -260,7 +275,8 @@ int dfs_bsa_fwd(const void* q_perm, const void* k_perm, const void* v_t,
                 int pv_dtype, float scale, void* out, int out_dtype,
                 const int32_t* out_perm, float* lse,
                 const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                int64_t n_seq, const int32_t* exps, dfs_stream_t stream);
+                int64_t n_seq, const int32_t* exps, const void* q_src,
+                const int32_t* q_rows, int q_src_dtype, dfs_stream_t stream);
 
 /* uint8/bool block mask [H][Qb][Kb] -> per-row counts int32 [H*Qb].
  * Part of the bool-mask interface of block_sparse_attn_func

@@ -59,10 +59,11 @@ def test_permute_gather_scatter_bit_exact(dev, dtype, d, length, n):
 
 
 @pytest.mark.parametrize("case", ["wan_tail", "wan_even", "hunyuan_text", "hunyuan_no_text", "d64_tile32",
-                                  "tile8", "d64_tile64", "q8_k64", "q128_k4_text", "d64_q64_k32"])
+                                  "tile8", "d64_tile64", "q8_k64", "q128_k4_text", "d64_q64_k32", "no_q_operand"])
 def test_prepare_qkv_matches_oracle(dev, case):
     heads, d, tile, dtype, pv = 2, 128, 16, torch.bfloat16, torch.float16
     k_tile = None
+    q_operand = case != "no_q_operand"
     if case == "wan_tail":
         length, video = 1000, 1000
     elif case == "wan_even":
@@ -81,6 +82,8 @@ def test_prepare_qkv_matches_oracle(dev, case):
         length, video, tile, k_tile = 1000 + 60, 1000, 128, 4
     elif case == "d64_q64_k32":
         length, video, d, tile, k_tile = 900, 900, 64, 64, 32
+    elif case == "no_q_operand":  # Q only pooled (the attention kernel reads it from the input)
+        length, video = 1000 + 60, 1000
     else:
         length, video, d, tile, pv = 777, 777, 64, 32, torch.bfloat16
     torch.manual_seed(7)
@@ -88,12 +91,16 @@ def test_prepare_qkv_matches_oracle(dev, case):
     vperm = torch.randperm(video)
     perm, _ = orc.full_permutation(vperm, length)
     layout = ScoringLayout(length, video, tile, k_tile=k_tile)
-    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout, operand_dtype=pv)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev, torch.int32), layout, operand_dtype=pv,
+                           q_operand=q_operand)
     qp, kp, vp = (orc.apply_permutation(x, perm) for x in (q, k, v))
     R = layout.rows
     pad = lambda x: torch.cat([x[0], x.new_zeros(heads, R - length, d)], dim=1)
-    assert prep.q_perm.dtype == pv and prep.k_perm.dtype == pv  # f16 operands: exact bf16 -> f16 rounding
-    assert torch.equal(prep.q_perm.cpu(), pad(qp).to(pv))
+    assert prep.k_perm.dtype == pv  # f16 operands: exact bf16 -> f16 rounding
+    if q_operand:
+        assert prep.q_perm.dtype == pv and torch.equal(prep.q_perm.cpu(), pad(qp).to(pv))
+    else:
+        assert prep.q_perm is None and prep.q_src is not None
     assert torch.equal(prep.k_perm.cpu(), pad(kp).to(pv))
     assert torch.equal(prep.v_t.cpu(), vt_reference(pad(vp), pv))
     if prep.exps is not None:  # bf16 inputs inside the f16 range: no head is rescaled
@@ -136,7 +143,8 @@ def test_prepare_rescales_heads_beyond_f16(dev):
 
 
 @pytest.mark.parametrize("pv", (torch.float16, torch.bfloat16))
-def test_bsa_fwd_keeps_inputs_beyond_f16(dev, pv):
+@pytest.mark.parametrize("q_operand", [True, False])
+def test_bsa_fwd_keeps_inputs_beyond_f16(dev, pv, q_operand):
     """Heads with q, k or v beyond the f16 range (q * scale * log2(e) beyond
     it too, so rows carry their own power of two) against fp32 masked
     attention of the same bf16 inputs."""
@@ -155,7 +163,8 @@ def test_bsa_fwd_keeps_inputs_beyond_f16(dev, pv):
     mask[:, torch.arange(nb), torch.arange(nb)] = True
     layout = ScoringLayout(length, length, 16)
     ident = torch.arange(length, dtype=torch.int32, device=dev)
-    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident, layout, operand_dtype=pv, pool=False)
+    prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), ident, layout, operand_dtype=pv, pool=False,
+                           q_operand=q_operand)
     row_ptr, col_idx = ops.mask_to_csr(mask.to(dev))
     got = ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=torch.float32).cpu()
     ref = orc.masked_attention(q, k, v, mask)
@@ -639,3 +648,54 @@ def test_bsa_fwd_varlen_rows_without_keys(dev, length, cu_q, cu_k, far_rows):
     assert bool((got[0][~live] == 0).all())
     assert bool(torch.isneginf(lse[~live]).all())
     assert bool(torch.isfinite(lse[live]).all())
+
+
+@pytest.mark.parametrize("case", ["bf16_d128", "f16_d64", "bf16_operands", "varlen", "q_beyond_f16"])
+def test_bsa_fwd_q_source_matches_q_perm(dev, case):
+    """dfs_bsa_fwd reading Q from the input through the permutation (q_src,
+    q_rows; dfs_prepare_qkv then writes no q_perm) against the same call on
+    the prepared q_perm and against fp32 masked attention: the two differ by
+    the rounding of Q * scale * log2(e) to f16 only (one rounding from the
+    input instead of two), and the second-sequence and scaled instances read
+    the same source."""
+    import math as _m
+    from dfsattn_amd.workloads import DfsConfig, synth_qkv
+    heads, d, length, dtype, pv = 3, 128, 1100, torch.bfloat16, torch.float16
+    cu = None
+    if case == "f16_d64":
+        d, dtype = 64, torch.float16
+    elif case == "bf16_operands":
+        pv = torch.bfloat16
+    elif case == "varlen":
+        cu = [0, 900, length]
+    cfg = DfsConfig("t", (1, 1, length), heads, d, torch.float32, seed=41)
+    q, k, v = synth_qkv(cfg)
+    if case == "q_beyond_f16":
+        q[:, 1] *= 3e5  # head 1's Q exceeds the f16 range: the scaled instance, rows shifted in the kernel
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    perm = torch.randperm(length, generator=torch.Generator().manual_seed(42)).to(torch.int32)
+    layout = ScoringLayout(length, length, 16)
+    nb = _m.ceil(length / 128)
+    mask = torch.rand((heads, nb, nb), generator=torch.Generator().manual_seed(43)) < 0.4
+    mask[:, torch.arange(nb), torch.arange(nb)] = True
+    row_ptr, col_idx = ops.mask_to_csr(mask.to(dev))
+    kw = {}
+    if cu is not None:
+        cu_d = torch.tensor(cu, dtype=torch.int32, device=dev)
+        kw = dict(cu_seqlens_q=cu_d, cu_seqlens_k=cu_d)
+    outs = {}
+    for q_operand in (True, False):
+        prep = ops.prepare_qkv(q.to(dev), k.to(dev), v.to(dev), perm.to(dev), layout, operand_dtype=pv,
+                               pool=False, q_operand=q_operand)
+        assert (prep.q_perm is None) == (not q_operand)
+        outs[q_operand] = ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=torch.float32, **kw).cpu()
+    qp, kp, vp = (orc.apply_permutation(x.float(), perm.long()) for x in (q, k, v))
+    ref = (orc.masked_attention(qp, kp, vp, mask) if cu is None else orc.varlen_attention(qp, kp, vp, mask, cu, cu))
+    for q_operand, out in outs.items():
+        ma, mr = float((out - ref).abs().max()), mean_rel(out, ref)
+        tol = 1e-3 if pv == torch.float16 else 3e-3
+        assert ma <= 2e-2 and mr <= tol, (q_operand, ma, mr)
+    if pv == torch.bfloat16 or dtype == torch.float16:
+        assert torch.equal(outs[True], outs[False])  # the same operand values either way
+    elif case != "q_beyond_f16":  # (there one-hot rows may pick another key on a rounding)
+        assert mean_rel(outs[False], outs[True]) < 5e-4

@@ -53,16 +53,25 @@ def test_abi_rejects_bad_arguments_without_launching():
         _lib.call("dfs_topk_from_scores", fake, 2, 8, 8, 8, 8, 9, 8, 8, fake, fake, None, None)
     with pytest.raises(_lib.DfsKernelError, match="f16 inputs"):
         _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 0, 0.1, fake, 2,
-                  None, None, None, None, 1, None, None)
+                  None, None, None, None, 1, None, None, None, 0, None)
     with pytest.raises(_lib.DfsKernelError, match="n_seq=3"):
         _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 1, 0.1, fake, 2,
-                  None, None, fake, fake, 3, None, None)
+                  None, None, fake, fake, 3, None, None, None, 0, None)
     with pytest.raises(_lib.DfsKernelError, match="both cu_seqlens_q and cu_seqlens_k"):
         _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 1, 0.1, fake, 2,
-                  None, None, fake, None, 2, None, None)
+                  None, None, fake, None, 2, None, None, None, 0, None)
     with pytest.raises(_lib.DfsKernelError, match="two sequences need cu_seqlens"):
         _lib.call("dfs_bsa_fwd", fake, fake, fake, fake, fake, 2, 1000, 128, 1, 1, 0.1, fake, 2,
-                  None, None, None, None, 2, None, None)
+                  None, None, None, None, 2, None, None, None, 0, None)
+    with pytest.raises(_lib.DfsKernelError, match="q_src needs q_rows"):
+        _lib.call("dfs_bsa_fwd", None, fake, fake, fake, fake, 2, 1000, 128, 1, 1, 0.1, fake, 2,
+                  None, None, None, None, 1, None, fake, None, 0, None)
+    with pytest.raises(_lib.DfsKernelError, match="bf16 Q/K operands need a bf16 q_src"):
+        _lib.call("dfs_bsa_fwd", None, fake, fake, fake, fake, 2, 1000, 128, 0, 0, 0.1, fake, 2,
+                  None, None, None, None, 1, None, fake, fake, 1, None)
+    with pytest.raises(_lib.DfsKernelError, match="NULL operand"):
+        _lib.call("dfs_bsa_fwd", None, fake, fake, fake, fake, 2, 1000, 128, 1, 1, 0.1, fake, 2,
+                  None, None, None, None, 1, None, None, None, 0, None)
     with pytest.raises(_lib.DfsKernelError, match="head_dim=96"):
         _lib.call("dfs_prepare_fixup", fake, fake, fake, fake, 2, 1000, 96, fake, fake, fake, fake, fake, None)
     # the allocation-free scorer refuses block sums beyond its 96 MiB scratch
@@ -219,8 +228,8 @@ def test_noalloc_wrapper_runs_under_the_tensors_device(monkeypatch):
     fake_t = SimpleNamespace(device=target)
     layout = ScoringLayout(1024, 1024, 16)
     pol = wan_policy(layout, 0.3)
-    prep = SimpleNamespace(q_hi=fake_t, q_lo=fake_t, k_hi=fake_t, k_lo=fake_t, q_perm=fake_t, heads=2,
-                           head_dim=64, layout=layout)
+    prep = SimpleNamespace(q_hi=fake_t, q_lo=fake_t, k_hi=fake_t, k_lo=fake_t, q_perm=None, k_perm=fake_t,
+                           device=target, heads=2, head_dim=64, layout=layout)
     real_empty = torch.empty
     monkeypatch.setattr(ops, "_require_device", lambda *a: None)
     monkeypatch.setattr(ops, "_require_int32", lambda **k: None)
