@@ -22,7 +22,9 @@ attention kernel time.
 
 The default line also carries the second BASELINE configuration under
 ``cfg2``: the HunyuanVideo call's time, phases and attention-kernel fraction
-of peak over 10 fresh-mask calls (skipped with ``--headline-only``).
+of peak over 10 fresh-mask calls; and under ``cfg4`` the 40-block DiT
+denoising step with DFS self-attention against the dense step (both skipped
+with ``--headline-only``).
 
 ``--workload cfg2`` measures the HunyuanVideo call instead (configs[2]:
 118,800 video + 256 text tokens, 24 heads), and ``--workload cfg3`` the
@@ -621,6 +623,17 @@ def main():
                 "call_ms": c2["value"], "attention_ms": c2["phases_ms"]["attention"],
                 "attention_tflops": c2["attention_kernel"]["tflops"], "attention_frac": c2["attention_kernel"]["frac"],
                 "call_frac": c2["frac_of_bf16_peak"], "phases_ms": c2["phases_ms"], "kept_flop": c2["kept_flop"]}
+    cfg4 = None
+    if not args.headline_only:
+        # the whole 40-block DiT denoising step (both CFG passes)
+        # with DFS self-attention at a mask-refresh step, beside the dense
+        # step, one timed step each after one untimed.
+        log("cfg4 (40-block DiT step) for the extra keys")
+        c4 = run_cfg4(argparse.Namespace(steps=1, warmup=1, dit_phase="both"))
+        torch.cuda.empty_cache()
+        cfg4 = {"workload": c4["config"]["workload"] + "; 1 timed step after 1 untimed",
+                "dfs_step_ms": c4["value"], "dense_step_ms": c4["dense_step_ms"],
+                "speedup_vs_dense": c4["speedup_vs_dense"], "params": c4["params"]}
     cpu = None if args.no_cpu_baseline else cpu_baseline(*inputs)
     del inputs
     att_ms = res["phase_ms"]["attention"]
@@ -653,6 +666,7 @@ def main():
         "kept_density": round(res["density"], 4),
         **res["side"],
         "cfg2": cfg2,
+        "cfg4": cfg4,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
