@@ -121,6 +121,63 @@ def test_full_size_call(dev, cfg_id):
     _dfs_attention_instances.clear()
 
 
+def test_full_size_tile32_and_bf16_operands(dev):
+    """configs[1] with the class's default tile of 32 tokens (the other
+    one-pass scorer instance): fp32 block scores of two heads against the
+    oracle and the selection from them; then the bf16-operand kernel (the
+    reference kernel's precision class) on that mask, sampled query blocks of
+    four heads against fp32 masked attention within its tolerance."""
+    from dfsattn_amd import ops
+    from dfsattn_amd.layout import ScoringLayout, wan_policy
+    from dfsattn_amd.utils.order import hilbert3d_perm
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[1]
+    q, k, v = synth_qkv(cfg, device=dev)
+    L, H = cfg.seq_len, cfg.heads
+    full, _ = orc.full_permutation(hilbert3d_perm(*cfg.grid), L)
+    perm_d = ops.device_perm(full, dev)
+    lay = ScoringLayout(L, L, 32)
+    pol = wan_policy(lay, cfg.sparsity)
+    prep = ops.prepare_qkv(q, k, v, perm_d, lay, q_operand=False)
+    row_ptr = torch.from_numpy(pol.row_ptr(H)).to(dev)
+    col_idx, scores, mask_d = ops.block_score_topk(prep, pol, row_ptr, want_scores=True, want_mask=True)
+    mask = mask_d.cpu().bool()
+    sh = [0, H - 1]
+    qp = orc.apply_permutation(q[:, sh].float().cpu(), full)
+    kp = orc.apply_permutation(k[:, sh].float().cpu(), full)
+    ref_scores = orc.block_scores(qp, kp, 32, 128, None, head_chunk=1)
+    got = scores[sh].cpu()
+    err = float((got.double() - ref_scores.double()).abs().max())
+    print(f"cfg1 tile 32 scores, heads {sh}: max abs error {err:.2e}", flush=True)
+    torch.testing.assert_close(got, ref_scores, rtol=1e-4, atol=1e-9)
+    assert torch.equal(mask[sh], orc.mask_from_scores_wan(got, cfg.sparsity))
+    kpick = orc.topk_count(cfg.sparsity, lay.k_blocks)
+    ref_sel = orc.mask_from_scores_wan(ref_scores, cfg.sparsity)
+    for i in range(len(sh)):
+        for r in range(ref_scores.shape[1]):
+            if not torch.equal(ref_sel[i, r], mask[sh[i], r]):
+                top = torch.sort(ref_scores[i, r], descending=True).values
+                assert float(top[kpick - 1] - top[kpick]) <= 2 * err
+
+    # the bf16-operand kernel on this mask
+    del prep
+    prep16 = ops.prepare_qkv(q, k, v, perm_d, lay, operand_dtype=torch.bfloat16, pool=False)
+    out32 = ops.bsa_fwd(prep16, row_ptr, col_idx, out_dtype=torch.float32)
+    heads = [0, H // 3, (2 * H) // 3, H - 1]
+    nq = lay.q_blocks
+    qbs = sorted({0, nq // 4, nq // 2, (3 * nq) // 4, nq - 1})
+    sub = [orc.apply_permutation(t[:, heads].float().cpu(), full) for t in (q, k, v)]
+    ref = orc.masked_attention(*sub, mask[heads], 128, q_blocks=qbs)
+    rows = torch.cat([torch.arange(b * 128, min((b + 1) * 128, L)) for b in qbs])
+    g32, r = out32[:, heads].cpu()[:, :, rows], ref[:, :, rows]
+    max_abs, mr = float((g32 - r).abs().max()), _rel(g32, r)
+    print(f"cfg1 bf16 operands, fp32 output, {len(heads)} heads x {len(qbs)} blocks: max-abs {max_abs:.2e}, "
+          f"mean-rel {mr:.2e}", flush=True)
+    # bf16 P and V: the reference kernel's precision class (about 1.5e-3)
+    assert max_abs <= 3e-2 and mr <= 3e-3
+
+
 def test_full_size_hunyuan_text_padding(dev):
     """configs[2] with 30 of the 256 text tokens valid (cu_seqlens [0, valid,
     L], replace_hyvideo.py:221-228): the mask is selected over the whole
