@@ -15,10 +15,10 @@ that the call's own phase recorder places around prepare, score + top-k and
 attention in every timed step. Two side measurements ride on the same line:
 the attention kernel on bf16 operands (the reference kernel's operand
 precision) over the same mask, beside the default f16 operands timed in the
-same stretch, and
-a less local mask at the same density (K drawn from a field of its own, so a
-row's kept blocks spread over the whole row): its whole-call median and its
-attention kernel time.
+same stretch; a less local mask at the same density (K drawn from a field of
+its own, so a row's kept blocks spread over the whole row): its whole-call
+median and its attention kernel time; and the dense path (``full_attention``
+in "flash" mode, every block kept) on the same inputs under ``dense_call``.
 
 The default line also carries the second BASELINE configuration under
 ``cfg2``: the HunyuanVideo call's time, phases and attention-kernel fraction
@@ -184,8 +184,9 @@ def run_gpu(args):
 
 
 def _side_measurements(args, cfg, dev, q, k, v, video_perm, layout, pol, perm_d, row_ptr, col_idx, flops, reps):
-    """The attention kernel on bf16 operands over the headline mask, and a
-    less local mask at the same density (whole call and attention kernel)."""
+    """The attention kernel on bf16 operands over the headline mask, a less
+    local mask at the same density (whole call and attention kernel), and the
+    dense path on the same inputs."""
     from dfsattn_amd import ops
     from dfsattn_amd.attention_wan import dfs_attention
     from dfsattn_amd.layout import csr_flops
@@ -252,11 +253,34 @@ def _side_measurements(args, cfg, dev, q, k, v, video_perm, layout, pol, perm_d,
     }
     log(f"less local mask: {less_local}")
     del prep_n, qn, kn, vn
+
+    # The dense path (full_attention in "flash" mode: warm-up steps, skip
+    # layers and periodic dense steps of the processors) on the same inputs:
+    # the same kernel with every block kept.
+    from dfsattn_amd.fullattention import full_attention
+    full_attention(q, k, v, mode="flash")
+    dense = []
+    for _ in range(3):
+        a, b = _events()
+        a.record()
+        full_attention(q, k, v, mode="flash")
+        b.record()
+        dense.append((a, b))
+    torch.cuda.synchronize()
+    dense_ms = float(np.mean([a.elapsed_time(b) for a, b in dense]))
+    dense_flop = 4.0 * L * L * cfg.head_dim * cfg.heads
+    dense_call = {"workload": "full_attention(mode='flash') on the cfg1 inputs: every block kept, 3 timed calls "
+                              "after 1 untimed",
+                  "call_ms": round(dense_ms, 3), "flop": dense_flop,
+                  "tflops": round(dense_flop / (dense_ms * 1e-3) / 1e12, 1),
+                  "frac": round(dense_flop / (dense_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    log(f"dense call: {dense_call}")
     return {
         "attention_bf16_operands": {"ms": round(bf16_ms, 3), "tflops": round(flops / (bf16_ms * 1e-3) / 1e12, 1),
                                     "frac": round(flops / (bf16_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                                     "f16_operands_ms_same_stretch": round(f16_ms, 3)},
         "less_local_mask": less_local,
+        "dense_call": dense_call,
     }
 
 
