@@ -178,6 +178,49 @@ def test_full_size_tile32_and_bf16_operands(dev):
     assert max_abs <= 3e-2 and mr <= 3e-3
 
 
+def test_full_size_dense_path(dev):
+    """The dense path at the configs[1] shape (full_attention in "flash"
+    mode, the processors' warm-up and skip-layer steps: the block-sparse
+    kernel with every block kept): sampled query rows of two heads against
+    fp32 dense attention on the host, on the call's bf16 output and on fp32
+    output of the same kernel."""
+    import math
+
+    from dfsattn_amd import ops
+    from dfsattn_amd.fullattention import dense_attention_native, full_attention
+    from dfsattn_amd.workloads import CONFIGS, synth_qkv
+
+    cfg = CONFIGS[1]
+    q, k, v = synth_qkv(cfg, device=dev)
+    L, H = cfg.seq_len, cfg.heads
+    out = full_attention(q, k, v, mode="flash")
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and out.shape == q.shape
+    heads = [1, H - 2]
+    g = torch.Generator().manual_seed(5)
+    rows = torch.cat([torch.arange(0, 128), torch.randint(128, L - 128, (384,), generator=g),
+                      torch.arange(L - 128, L)])
+    qs = q[0, heads].float().cpu()[:, rows]
+    ks, vs = k[0, heads].float().cpu(), v[0, heads].float().cpu()
+    ref = torch.softmax((qs @ ks.transpose(-1, -2).contiguous()) / math.sqrt(cfg.head_dim), -1) @ vs
+    got = out[0, heads].cpu()[:, rows].float()
+    assert float((got - ref).abs().max()) < 2e-2 and _rel(got, ref) < 4e-3
+    # full_attention without cu_seqlens is dense_attention_native: the same bits
+    assert torch.equal(dense_attention_native(q, k, v), out)
+    from dfsattn_amd.layout import ScoringLayout, dense_policy
+    lay = ScoringLayout(L, L, 16)
+    pol = dense_policy(lay)
+    prep = ops.prepare_qkv(q, k, v, torch.arange(L, dtype=torch.int32, device=dev), lay, pool=False,
+                           q_operand=False)
+    row_ptr = torch.from_numpy(pol.row_ptr(H)).to(dev)
+    col_idx = torch.arange(pol.k_blocks, dtype=torch.int32, device=dev).repeat(H * pol.q_blocks)
+    f32 = ops.bsa_fwd(prep, row_ptr, col_idx, out_dtype=torch.float32)[0, heads].cpu()[:, rows]
+    max_abs, mr = float((f32 - ref).abs().max()), _rel(f32, ref)
+    print(f"cfg1 dense path, fp32 output, {len(heads)} heads x {len(rows)} rows: max-abs {max_abs:.2e}, "
+          f"mean-rel {mr:.2e}", flush=True)
+    assert max_abs <= 2e-2 and mr <= 5e-4
+
+
 def test_full_size_hunyuan_text_padding(dev):
     """configs[2] with 30 of the 256 text tokens valid (cu_seqlens [0, valid,
     L], replace_hyvideo.py:221-228): the mask is selected over the whole
